@@ -1,0 +1,202 @@
+/*
+ * tmopt_attn.h — C ABI of the MI355X (gfx950) paged-attention library
+ * libtmopt_attn.so.
+ *
+ * This is the drop-in boundary for tm-opt's paged attention path. Every entry
+ * point takes plain device pointers, sizes and strides plus a hipStream_t; no
+ * C++ or torch types cross the boundary. Conventions shared by all entry
+ * points:
+ *
+ *   - Return value: 0 (TMOPT_OK) or a negative tmopt_status. Nothing aborts.
+ *     tmopt_last_error() returns a thread-local description of the last
+ *     failure on the calling thread.
+ *   - Nothing allocates device memory. Scratch space is passed in through a
+ *     `workspace` argument whose size the matching *_workspace_size query
+ *     returns, so every call is legal inside hipGraph stream capture.
+ *   - Every launch goes to the given stream; no host synchronisation.
+ *   - Tensors are bf16 unless stated. Index tensors are int32 (block tables,
+ *     lengths, cu_seqlens) or int64 (flat slot mappings).
+ *   - KV pools are [num_pages, page_size, HKV, D] bf16, contiguous: one page
+ *     holds page_size consecutive token rows, each row HKV*D elements. A pool
+ *     row index is page * page_size + offset.
+ *   - Results are deterministic: fixed reduction order, no atomics.
+ *
+ * Supported shapes: D == 128, page_size == 16, HQ % HKV == 0 with
+ * REP = HQ / HKV in {1, 2, 4, 8, 16} for decode and {4, 8} for prefill.
+ * Other shapes return TMOPT_EUNSUPPORTED.
+ */
+#ifndef TMOPT_ATTN_H
+#define TMOPT_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t is an opaque pointer; declared here without HIP headers so
+ * that host-only callers (ctypes, cgo, plain C) can include this file. */
+typedef struct ihipStream_t* tmopt_stream_t;
+
+typedef enum {
+  TMOPT_OK = 0,
+  TMOPT_EINVAL = -1,       /* bad pointer, size or stride */
+  TMOPT_EUNSUPPORTED = -2, /* shape outside the supported set above */
+  TMOPT_EWORKSPACE = -3,   /* workspace missing or too small */
+  TMOPT_ELAUNCH = -4       /* hipLaunchKernel / hipGetLastError failure */
+} tmopt_status;
+
+/* Thread-local text of the last error raised on this thread ("" if none). */
+const char* tmopt_last_error(void);
+
+/* Library version string, e.g. "tmopt_attn 0.1 gfx950". */
+const char* tmopt_version(void);
+
+/* ------------------------------------------------------------------------ */
+/* KV-cache write                                                           */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Scatter T token rows of K and V into the pools by flat row index.
+ * Replaces the reference's torch index_put_ appends
+ *   pool.kp.view(-1, HK, D)[flat_new] = k   (engine/pyengine/model.py:941-942)
+ *   pool.k[slots, ring_slot] = k            (engine/pyengine/model.py:947-948)
+ *   self.kp.view(-1, H, D)[slots] = k       (engine/pyengine/kv.py:203-204)
+ * k, v:          [T, HKV, D] with element strides (k_stride_tok,
+ *                k_stride_head); the D axis must be contiguous.
+ * slot_mapping:  [T] int64 flat pool rows; a negative entry skips the token.
+ *                Rows >= pool_rows are skipped as well (never written).
+ * k_pool,v_pool: [pool_rows, HKV, D] contiguous.
+ * Bit-exact copy. Duplicate rows in one call are written in unspecified
+ * order (the same contract as index_put_ without accumulate).
+ */
+int tmopt_kv_write_slots(const void* k, const void* v, int64_t k_stride_tok,
+                         int64_t k_stride_head, int64_t v_stride_tok,
+                         int64_t v_stride_head, const int64_t* slot_mapping,
+                         int64_t T, int HKV, int D, void* k_pool, void* v_pool,
+                         int64_t pool_rows, tmopt_stream_t stream);
+
+/*
+ * Append varlen token runs through a block table, computing each row's page
+ * in-kernel. Replaces PagedKV.append / RingKV.append
+ * (engine/pyengine/kv.py:193-205, :89-103) and the decode-step append
+ * (engine/pyengine/model.py:938-948) without the torch index math.
+ * Token t of sequence i (cu_seqlens[i] <= t < cu_seqlens[i+1]) sits at
+ * logical position start_pos[i] + (t - cu_seqlens[i]); its pool row is
+ *   table[i][lp] * page_size + pos % page_size,  lp = pos / page_size,
+ * with lp taken modulo table_wrap when table_wrap > 0 (ring pools: a
+ * sequence owns table_wrap pages that are reused cyclically). With
+ * table_wrap > 0 a token that a later token of the same call would
+ * overwrite is dropped, as RingKV.append does (kv.py:97-98).
+ * cu_seqlens may be NULL: then sequence i has exactly one token, k row i
+ * (the decode step). max_seqlen bounds the per-sequence token count.
+ * Table entries outside [0, num_pages) are skipped, never dereferenced.
+ */
+int tmopt_kv_write_paged(const void* k, const void* v, int64_t k_stride_tok,
+                         int64_t k_stride_head, int64_t v_stride_tok,
+                         int64_t v_stride_head, const int32_t* cu_seqlens,
+                         const int32_t* start_pos, int num_seqs, int max_seqlen,
+                         const int32_t* block_table, int64_t bt_stride,
+                         int table_wrap, int page_size, int HKV, int D,
+                         void* k_pool, void* v_pool, int64_t num_pages,
+                         tmopt_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Paged decode attention (split-KV + LSE combine)                          */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Bytes of workspace tmopt_attn_decode_paged needs for a given launch shape.
+ * max_splits = ceil(max visible pages / split_pages); see below.
+ */
+size_t tmopt_attn_decode_workspace_size(int B, int HQ, int D, int max_splits);
+
+/*
+ * One query token per sequence against its paged KV history. Replaces
+ * _attn_decode_kernel (engine/pyengine/kernels/attn_swa.py:49-117) behind
+ * attn_swa (attn_swa.py:120-141) and attn_global
+ * (engine/pyengine/kernels/attn_global.py:15-38), and the unimplemented
+ * native stub tmopt::kernels::decode_attention
+ * (engine/include/tmopt/kernels.h:33-35).
+ *
+ * q:            [B, HQ, D] contiguous; query of sequence b sits at position
+ *               ctx_lens[b] - 1.
+ * k_pool,v_pool:[num_pages, page_size, HKV, D] contiguous.
+ * block_table:  [B, bt_stride] int32 physical page ids; logical page lp of
+ *               sequence b is block_table[b*bt_stride + (table_wrap ?
+ *               lp % table_wrap : lp)]. Only pages holding visible keys are
+ *               read; entries outside [0, num_pages) are never dereferenced
+ *               (their keys count as absent).
+ * ctx_lens:     [B] int32 keys in the cache including the current token.
+ * window:       0 = global; W > 0 = sliding window, keys k with
+ *               pos - k < W only (pages wholly outside are never read).
+ * scale:        softmax scale applied to q.k.
+ * rel, rel_extent: optional fused relative bias (NULL = off): rel is
+ *               [B, HQ, rel_extent] contiguous and the score of key k gets
+ *               rel[b, h, dist] for 0 <= dist = pos - k < rel_extent, else 0
+ *               (attn_swa.py:97-102).
+ * split_pages:  pages per split (> 0). max_splits must be >= the number of
+ *               splits any sequence needs; the grid is fixed by it, so one
+ *               value per hipGraph bucket keeps captures static.
+ * out:          [B, HQ, D] bf16; lse: [B, HQ] fp32 natural-log sum-exp of
+ *               the scaled scores (may be NULL).
+ * workspace:    device scratch of tmopt_attn_decode_workspace_size bytes
+ *               (may be NULL when max_splits == 1).
+ */
+int tmopt_attn_decode_paged(const void* q, const void* k_pool,
+                            const void* v_pool, const int32_t* block_table,
+                            int64_t bt_stride, int table_wrap,
+                            const int32_t* ctx_lens, int B, int HQ, int HKV,
+                            int D, int page_size, int64_t num_pages,
+                            int window, float scale, const void* rel,
+                            int rel_extent, int split_pages, int max_splits,
+                            void* out, float* lse, void* workspace,
+                            size_t workspace_bytes, tmopt_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Varlen causal prefill attention (bf16 MFMA)                              */
+/* ------------------------------------------------------------------------ */
+
+/*
+ * Causal (optionally windowed) attention for packed variable-length query
+ * runs. Replaces _attn_prefill_kernel
+ * (engine/pyengine/kernels/attn_prefill.py:71-141) behind attn_prefill_fused
+ * (attn_prefill.py:144-194); the padded [B,H,T,D] form becomes cu_seqlens
+ * packing, and chunked prefill reads prior context from the paged cache.
+ *
+ * q:      [total_q, HQ, D] with element strides (q_stride_tok,
+ *         q_stride_head), D contiguous. Query j of sequence i (row
+ *         cu_seqlens_q[i] + j) sits at position prior_lens[i] + j
+ *         (prior_lens NULL = all zero).
+ * Keys of sequence i are positions [0, prior_lens[i] + len_i). They come
+ * from one of two sources:
+ *   block_table == NULL: packed k, v [total_q, HKV, D] (strides as q) hold
+ *         the run's own keys; prior_lens must be NULL.
+ *   block_table != NULL: every key is read from the paged pools
+ *         (k_pool, v_pool, [num_pages, page_size, HKV, D]) through
+ *         block_table [num_seqs, bt_stride]; the run's new keys must already
+ *         be written (tmopt_kv_write_paged), k and v are ignored.
+ * window: 0 = causal; W > 0 adds pos_q - pos_k < W. Key tiles wholly
+ *         outside the causal/window band are skipped.
+ * max_seqlen_q bounds every len_i (it sizes the grid).
+ * out:    [total_q, HQ, D] with element strides (o_stride_tok,
+ *         o_stride_head), D contiguous.
+ * lse:    [HQ, total_q] fp32 natural-log sum-exp of the scaled scores, or
+ *         NULL.
+ */
+int tmopt_attn_prefill_varlen(
+    const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k,
+    int64_t k_stride_tok, int64_t k_stride_head, const void* v,
+    int64_t v_stride_tok, int64_t v_stride_head, const int32_t* cu_seqlens_q,
+    const int32_t* prior_lens, int num_seqs, int max_seqlen_q,
+    const void* k_pool, const void* v_pool, const int32_t* block_table,
+    int64_t bt_stride, int page_size, int64_t num_pages, int HQ, int HKV, int D,
+    int window, float scale, void* out, int64_t o_stride_tok,
+    int64_t o_stride_head, float* lse, tmopt_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TMOPT_ATTN_H */

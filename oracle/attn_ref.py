@@ -1,0 +1,154 @@
+"""fp32 CPU oracle of the paged attention math (TEST INFRASTRUCTURE ONLY —
+see oracle/__init__.py; never imported by the product path).
+
+Every function computes in float32 from the bf16 inputs upcast exactly (not
+regenerated), which is the BASELINE oracle: softmax(scale * Q K^T + bias +
+mask) V with a natural-log LSE. The reference rounds the probabilities to
+bf16 before P.V (engine/pyengine/kernels/attn_swa.py:110-112); the oracle
+does not, and the tolerance absorbs that rounding.
+"""
+import math
+
+import torch
+
+PAGE = 16
+
+
+def _key_rows(block_table_row, positions, table_wrap, page=PAGE):
+    """Logical positions -> (physical page, in-page offset), following
+    PagedKV._flat_slots (engine/pyengine/kv.py:161-168); a ring table of
+    table_wrap pages reuses its pages cyclically (RingKV slot p % W,
+    kv.py:75-76 and :99-100, with W = table_wrap * page)."""
+    lp = positions // page
+    if table_wrap:
+        lp = lp % table_wrap
+    pages = block_table_row[lp].to(torch.int64)
+    return pages, positions % page
+
+
+def rel_bias_gather(rel_row, dist):
+    """rel[b, h, clamp(dist, 0, E-1)] zeroed outside 0 <= dist < E
+    (engine/pyengine/model.py:137-158 steps #2-#4; attn_swa.py:97-102).
+    rel_row [H, E] -> [H, len(dist)] fp32."""
+    E = rel_row.shape[-1]
+    idx = dist.clamp(0, E - 1)
+    g = rel_row.float()[:, idx]
+    band = (dist >= 0) & (dist < E)
+    return torch.where(band[None, :], g, torch.zeros((), dtype=g.dtype))
+
+
+def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
+                 table_wrap=0, rel=None):
+    """One query per sequence at position n-1 against its cached keys.
+
+    Follows _attn_decode_kernel (engine/pyengine/kernels/attn_swa.py:57-117)
+    and the eager chain it replaced (engine/pyengine/model.py:978-1014):
+    visible keys are positions [lo, n) with lo = max(0, n - W) on windowed
+    layers (attn_swa.py:71-72, :83-85: live iff 0 <= pos - p < W) and 0 on
+    global ones (:90-91: live iff l < n); GQA head h reads KV head h // REP
+    (model.py:995-998); score = q.k * scale + bias, softmax in fp32.
+
+    q [B, HQ, D]; pools [P, 16, HKV, D]; block_table [B, >=pages] int;
+    ctx_lens [B] int. Returns (out [B, HQ, D] fp32, lse [B, HQ] fp32)."""
+    B, HQ, D = q.shape
+    HKV = k_pool.shape[2]
+    rep = HQ // HKV
+    out = torch.zeros((B, HQ, D), dtype=torch.float32)
+    lse = torch.full((B, HQ), -math.inf, dtype=torch.float32)
+    bt = block_table.cpu()
+    for b in range(B):
+        n = int(ctx_lens[b])
+        if n <= 0:
+            continue
+        lo = max(0, n - window) if window else 0
+        pos = torch.arange(lo, n, dtype=torch.int64)
+        pages, offs = _key_rows(bt[b], pos, table_wrap)
+        K = k_pool[pages, offs].float()            # [n_vis, HKV, D]
+        V = v_pool[pages, offs].float()
+        Kh = K.repeat_interleave(rep, dim=1)       # [n_vis, HQ, D]
+        Vh = V.repeat_interleave(rep, dim=1)
+        qb = q[b].float()                          # [HQ, D]
+        s = torch.einsum("hd,nhd->hn", qb, Kh) * scale
+        if rel is not None:
+            s = s + rel_bias_gather(rel[b].cpu(), (n - 1) - pos)
+        lse[b] = torch.logsumexp(s, dim=-1)
+        p = torch.softmax(s, dim=-1)
+        out[b] = torch.einsum("hn,nhd->hd", p, Vh)
+    return out, lse
+
+
+def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, prior_lens=None,
+                   k_pool=None, v_pool=None, block_table=None, q_block=256):
+    """Causal (optionally windowed) attention over packed runs.
+
+    Follows _attn_prefill_kernel (engine/pyengine/kernels/attn_prefill.py:
+    80-141) and the eager chain of attn_prefill (engine/pyengine/model.py:
+    530-556): query j of run i sits at position p_i + j (p_i = prior tokens),
+    keys at positions 0..p_i+len_i-1, kept iff 0 <= qpos - kpos (< W on
+    windowed layers) — the additive_causal_mask predicate (model.py:228-246).
+    GQA head h reads KV head h // REP. Prior keys (and, when block_table is
+    given, all keys) come from the paged pools through the table; otherwise
+    the run's own keys are the packed k/v rows.
+
+    Returns (out [total, HQ, D] fp32, lse [HQ, total] fp32)."""
+    total, HQ, D = q.shape
+    cu = cu_seqlens.to(torch.int64).cpu()
+    S = cu.shape[0] - 1
+    if block_table is not None:
+        HKV = k_pool.shape[2]
+    else:
+        HKV = k.shape[1]
+    rep = HQ // HKV
+    out = torch.zeros((total, HQ, D), dtype=torch.float32)
+    lse = torch.full((HQ, total), -math.inf, dtype=torch.float32)
+    for i in range(S):
+        t0, t1 = int(cu[i]), int(cu[i + 1])
+        T = t1 - t0
+        if T <= 0:
+            continue
+        p0 = 0 if prior_lens is None else int(prior_lens[i])
+        nk = p0 + T
+        if block_table is not None:
+            kpos = torch.arange(nk, dtype=torch.int64)
+            pages, offs = _key_rows(block_table[i].cpu(), kpos, 0)
+            K = k_pool[pages, offs].float()
+            V = v_pool[pages, offs].float()
+        else:
+            assert p0 == 0
+            K = k[t0:t1].float()
+            V = v[t0:t1].float()
+        Kh = K.repeat_interleave(rep, dim=1).permute(1, 0, 2)   # [HQ, nk, D]
+        Vh = V.repeat_interleave(rep, dim=1).permute(1, 0, 2)
+        for j0 in range(0, T, q_block):
+            j1 = min(T, j0 + q_block)
+            qp = p0 + torch.arange(j0, j1, dtype=torch.int64)
+            k_lo = max(0, p0 + j0 - window + 1) if window else 0
+            k_hi = p0 + j1                       # exclusive
+            kp = torch.arange(k_lo, k_hi, dtype=torch.int64)
+            qb = q[t0 + j0:t0 + j1].float().permute(1, 0, 2)    # [HQ, m, D]
+            s = torch.matmul(qb, Kh[:, k_lo:k_hi].transpose(1, 2)) * scale
+            d = qp[:, None] - kp[None, :]
+            keep = d >= 0
+            if window:
+                keep &= d < window
+            s = s.masked_fill(~keep[None], -math.inf)
+            lse[:, t0 + j0:t0 + j1] = torch.logsumexp(s, dim=-1)
+            p = torch.softmax(s, dim=-1)
+            out[t0 + j0:t0 + j1] = torch.matmul(
+                p, Vh[:, k_lo:k_hi]).permute(1, 0, 2)
+    return out, lse
+
+
+def decode_reference_semantics(q, pool_k, pool_v, slots, pos, rel, window):
+    """attn_swa's model semantics (engine/pyengine/kernels/attn_swa.py:
+    120-141): ring pool [S, W, HK, D], scale 1/D, rel extent == W.
+    Restated through the paged oracle with the ring viewed as pages."""
+    B, HQ, D = q.shape
+    S, W, HK, _ = pool_k.shape
+    per = W // PAGE
+    kp = pool_k.reshape(S * per, PAGE, HK, D)
+    vp = pool_v.reshape(S * per, PAGE, HK, D)
+    table = slots.to(torch.int64)[:, None] * per + torch.arange(per)[None]
+    ctx = pos.to(torch.int64) + 1
+    return decode_paged(q, kp, vp, table, ctx, 1.0 / D, window=W,
+                        table_wrap=per, rel=rel)

@@ -1,0 +1,161 @@
+"""Parity of the HIP split-KV paged decode kernel against the fp32 oracle.
+
+Tolerances (BASELINE): outputs max-abs 2e-2 / rtol 1e-2, LSE 1e-3. Pools are
+NaN-poisoned outside the pages a sequence owns, so any stray read shows up
+as a non-finite output. Geometry edges follow the reference's own arm
+(engine/pyengine/tests/t_fused_attn.py:119-122): positions 0, 3, 200, 511,
+512, 513, 800, 1500 and a dead row at position 0.
+"""
+import math
+
+import pytest
+import torch
+
+from helpers import assert_lse_close, assert_out_close
+from oracle import attn_ref
+
+pytestmark = pytest.mark.gpu
+
+EDGE_POS = [0, 3, 200, 511, 512, 513, 800, 1500, 0]
+
+
+def _run(tm, case, dev, **kw):
+    c = case.to(dev)
+    out, lse = tm.decode_paged(c.q, c.k_pool, c.v_pool, c.block_table,
+                               c.ctx_lens, c.scale, window=c.window, **kw)
+    torch.cuda.synchronize()
+    return out.cpu(), lse.cpu()
+
+
+def _oracle(case, **kw):
+    return attn_ref.decode_paged(case.q, case.k_pool, case.v_pool,
+                                 case.block_table, case.ctx_lens, case.scale,
+                                 window=case.window, **kw)
+
+
+def test_config1_global_decode(tm, dev):
+    from importlib import import_module
+    wl = import_module("tm-opt_amd.workloads")
+    case = wl.config1(poison=True)
+    ref_o, ref_l = _oracle(case)
+    out, lse = _run(tm, case, dev)
+    assert_out_close(out, ref_o, "C1")
+    assert_lse_close(lse, ref_l, "C1")
+
+
+@pytest.mark.parametrize("window", [0, 512])
+@pytest.mark.parametrize("split_pages", [1, 3, 16, 128])
+def test_edge_positions(tm, dev, window, split_pages):
+    from importlib import import_module
+    wl = import_module("tm-opt_amd.workloads")
+    case = wl.make_decode("edges", 7, len(EDGE_POS), 0, 0, window,
+                          ctx=[p + 1 for p in EDGE_POS])
+    ref_o, ref_l = _oracle(case)
+    out, lse = _run(tm, case, dev, split_pages=split_pages)
+    assert_out_close(out, ref_o, f"edges w={window} sp={split_pages}")
+    assert_lse_close(lse, ref_l, f"edges w={window} sp={split_pages}")
+
+
+@pytest.mark.parametrize("hq,hkv", [(64, 8), (64, 16), (32, 4), (16, 16),
+                                    (32, 2)])
+def test_gqa_shapes(tm, dev, hq, hkv):
+    from importlib import import_module
+    wl = import_module("tm-opt_amd.workloads")
+    case = wl.make_decode("gqa", 8, 6, 1, 700, 0, hq=hq, hkv=hkv)
+    ref_o, ref_l = _oracle(case)
+    out, lse = _run(tm, case, dev, split_pages=8)
+    assert_out_close(out, ref_o, f"gqa {hq}/{hkv}")
+    assert_lse_close(lse, ref_l, f"gqa {hq}/{hkv}")
+
+
+def test_window_only_reads_window_pages(tm, dev):
+    """Pages before the window point at a NaN poison page; output finite and
+    equal to the oracle (which never touches them either)."""
+    from importlib import import_module
+    wl = import_module("tm-opt_amd.workloads")
+    case = wl.make_decode("swa", 9, 12, 700, 5000, window=1000)
+    assert (case.block_table == case.meta["pool_pages"] - 1).any()
+    ref_o, ref_l = _oracle(case)
+    out, lse = _run(tm, case, dev, split_pages=5)
+    assert_out_close(out, ref_o, "swa")
+    assert_lse_close(lse, ref_l, "swa")
+
+
+def test_split_invariance_and_determinism(tm, dev):
+    from importlib import import_module
+    wl = import_module("tm-opt_amd.workloads")
+    case = wl.make_decode("inv", 10, 5, 900, 3000)
+    outs = []
+    for sp in (1, 2, 7, 64, 256):
+        outs.append(_run(tm, case, dev, split_pages=sp))
+    base_o, base_l = outs[-1]          # single split per sequence
+    for o, l in outs[:-1]:
+        assert (o.float() - base_o.float()).abs().max() <= 2 * 2 ** -8 * \
+            base_o.float().abs().max()
+        assert (l - base_l).abs().max() <= 1e-4
+    again = _run(tm, case, dev, split_pages=7)
+    assert torch.equal(again[0], outs[2][0]) and torch.equal(again[1],
+                                                            outs[2][1])
+
+
+def test_zero_query_closed_form(tm, dev):
+    """q = 0: uniform weights, LSE = ln(n_visible), out = mean of visible V."""
+    from importlib import import_module
+    wl = import_module("tm-opt_amd.workloads")
+    case = wl.make_decode("q0", 11, 7, 1, 2000, window=333)
+    case.q.zero_()
+    out, lse = _run(tm, case, dev, split_pages=4)
+    nv = case.visible().double()
+    assert torch.allclose(lse.double(), torch.log(nv)[:, None].expand_as(lse),
+                          atol=1e-4, rtol=0)
+    ref_o, _ = _oracle(case)
+    assert_out_close(out, ref_o, "q=0")
+
+
+def test_rel_bias_and_ring_table(tm, dev):
+    """The reference's SWA model semantics (attn_swa.py:120-141): ring pool
+    [S, W, HK, D] viewed as pages, scale 1/D, fused rel bias of extent W."""
+    g = torch.Generator().manual_seed(5)
+    S, W, HK, D, HQ = 6, 512, 16, 128, 64
+    pool_k = torch.randn((S + 1, W, HK, D), generator=g).to(torch.bfloat16)
+    pool_v = torch.randn((S + 1, W, HK, D), generator=g).to(torch.bfloat16)
+    pos = torch.tensor([0, 3, 200, 511, 512, 513, 800, 0])
+    slots = torch.tensor([4, 0, 2, 5, 1, 3, 6, 6])
+    B = pos.shape[0]
+    q = torch.randn((B, HQ, D), generator=g).to(torch.bfloat16)
+    rel = (torch.randn((B, HQ, W), generator=g) * 0.5).to(torch.bfloat16)
+    ref_o, ref_l = attn_ref.decode_reference_semantics(q, pool_k, pool_v,
+                                                       slots, pos, rel, W)
+    per = W // 16
+    kp = pool_k.view((S + 1) * per, 16, HK, D).to(dev)
+    vp = pool_v.view((S + 1) * per, 16, HK, D).to(dev)
+    table = (slots[:, None] * per + torch.arange(per)[None]).to(torch.int32)
+    out, lse = tm.decode_paged(q.to(dev), kp, vp, table.to(dev),
+                               (pos + 1).to(torch.int32).to(dev), 1.0 / D,
+                               window=W, table_wrap=per, rel=rel.to(dev),
+                               split_pages=8)
+    torch.cuda.synchronize()
+    assert_out_close(out, ref_o, "ring+rel")
+    assert_lse_close(lse, ref_l, "ring+rel")
+
+
+def test_empty_and_zero_length(tm, dev):
+    """B == 0 is a no-op; a zero-length sequence yields 0 and LSE -inf."""
+    from importlib import import_module
+    wl = import_module("tm-opt_amd.workloads")
+    case = wl.make_decode("z", 12, 3, 5, 50)
+    c = case.to(dev)
+    c.ctx_lens[1] = 0
+    out, lse = tm.decode_paged(c.q, c.k_pool, c.v_pool, c.block_table,
+                               c.ctx_lens, c.scale, split_pages=1)
+    torch.cuda.synchronize()
+    assert torch.all(out[1].float() == 0)
+    assert torch.all(torch.isinf(lse[1])) and torch.all(lse[1] < 0)
+    ref_o, ref_l = attn_ref.decode_paged(case.q, case.k_pool, case.v_pool,
+                                         case.block_table,
+                                         c.ctx_lens.cpu(), case.scale)
+    assert_out_close(out, ref_o, "zero-len")
+    e = tm.decode_paged(c.q[:0], c.k_pool, c.v_pool, c.block_table[:0],
+                        c.ctx_lens[:0], c.scale)
+    assert e[0].shape == (0, 32, 128)
+    assert math.isfinite(float(lse[0].max()))

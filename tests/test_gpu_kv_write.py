@@ -1,0 +1,166 @@
+"""Bit-exact parity of the HIP KV-cache write against the numpy oracle.
+
+Covers the flat slot-mapping form (index_put_ semantics, model.py:941-948),
+the block-table form for prefill runs, decode steps and ring pools, strided
+inputs, skipped rows, and the reference's structural pins restated from
+engine/pyengine/tests/t_b3.py:81-130.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import kv_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16(shape, g):
+    return torch.randn(shape, generator=g).to(torch.bfloat16)
+
+
+def test_write_slots_matches_index_put(tm, dev):
+    g = torch.Generator().manual_seed(11)
+    T, H, D, P = 37, 4, 128, 40
+    k = _bf16((T, H, D), g)
+    v = _bf16((T, H, D), g)
+    kp = _bf16((P, 16, H, D), g)
+    vp = _bf16((P, 16, H, D), g)
+    slots = torch.randperm(P * 16, generator=g)[:T].to(torch.int64)
+    slots[::7] = -1                       # skipped rows
+    slots[3] = P * 16 + 5                 # beyond the pool: skipped
+    want_k = kv_ref.write_slots(kv_ref.as_u16(kp).copy(), kv_ref.as_u16(k),
+                                slots.numpy())
+    want_v = kv_ref.write_slots(kv_ref.as_u16(vp).copy(), kv_ref.as_u16(v),
+                                slots.numpy())
+    kd, vd = kp.to(dev), vp.to(dev)
+    tm.kv_write_slots(k.to(dev), v.to(dev), slots.to(dev), kd, vd)
+    torch.cuda.synchronize()
+    assert np.array_equal(kv_ref.as_u16(kd), want_k)
+    assert np.array_equal(kv_ref.as_u16(vd), want_v)
+
+
+def test_write_slots_strided_input(tm, dev):
+    g = torch.Generator().manual_seed(12)
+    T, H, D, P = 20, 4, 128, 8
+    big = _bf16((T, H, 2 * D), g)
+    k = big[:, :, :D]                      # head stride 256, token 1024
+    v = big[:, :, D:]
+    assert not k.is_contiguous()
+    kp = torch.zeros((P, 16, H, D), dtype=torch.bfloat16)
+    vp = torch.zeros_like(kp)
+    slots = torch.randperm(P * 16, generator=g)[:T].to(torch.int64)
+    want_k = kv_ref.write_slots(kv_ref.as_u16(kp).copy(),
+                                kv_ref.as_u16(k.contiguous()), slots.numpy())
+    want_v = kv_ref.write_slots(kv_ref.as_u16(vp).copy(),
+                                kv_ref.as_u16(v.contiguous()), slots.numpy())
+    bd = big.to(dev)
+    kd, vd = kp.to(dev), vp.to(dev)
+    tm.kv_write_slots(bd[:, :, :D], bd[:, :, D:], slots.to(dev), kd, vd)
+    torch.cuda.synchronize()
+    assert np.array_equal(kv_ref.as_u16(kd), want_k)
+    assert np.array_equal(kv_ref.as_u16(vd), want_v)
+
+
+@pytest.mark.parametrize("wrap", [0, 3])
+def test_write_paged_varlen(tm, dev, wrap):
+    g = torch.Generator().manual_seed(13 + wrap)
+    H, D = 4, 128
+    lens = [5, 33, 16, 1, 70]
+    start = [0, 7, 100, 3, 20]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    k = _bf16((T, H, D), g)
+    v = _bf16((T, H, D), g)
+    need = 10 if not wrap else wrap
+    P = 64
+    perm = torch.randperm(P, generator=g)
+    table = perm[:len(lens) * need].view(len(lens), need).to(torch.int32)
+    table[0, 0] = P + 3                    # invalid entry: never written
+    kp = _bf16((P, 16, H, D), g)
+    vp = _bf16((P, 16, H, D), g)
+    want_k = kv_ref.write_paged(kv_ref.as_u16(kp).copy(), kv_ref.as_u16(k),
+                                cu, start, table.numpy(), 16, wrap)
+    want_v = kv_ref.write_paged(kv_ref.as_u16(vp).copy(), kv_ref.as_u16(v),
+                                cu, start, table.numpy(), 16, wrap)
+    kd, vd = kp.to(dev), vp.to(dev)
+    tm.kv_write_paged(k.to(dev), v.to(dev), table.to(dev),
+                      torch.tensor(start, dtype=torch.int32, device=dev), kd,
+                      vd, cu_seqlens=torch.from_numpy(cu).to(dev),
+                      table_wrap=wrap)
+    torch.cuda.synchronize()
+    assert np.array_equal(kv_ref.as_u16(kd), want_k)
+    assert np.array_equal(kv_ref.as_u16(vd), want_v)
+
+
+def test_write_paged_decode_step(tm, dev):
+    """One token per sequence at position ctx-1 (model.py:938-948)."""
+    g = torch.Generator().manual_seed(21)
+    B, H, D, P, npg = 9, 4, 128, 128, 8
+    k = _bf16((B, H, D), g)
+    v = _bf16((B, H, D), g)
+    table = torch.randperm(P, generator=g)[:B * npg].view(B, npg).to(
+        torch.int32)
+    pos = torch.tensor([0, 3, 15, 16, 17, 63, 64, 100, 127], dtype=torch.int32)
+    kp = _bf16((P, 16, H, D), g)
+    vp = _bf16((P, 16, H, D), g)
+    want_k = kv_ref.write_paged(kv_ref.as_u16(kp).copy(), kv_ref.as_u16(k),
+                                None, pos.numpy(), table.numpy())
+    want_v = kv_ref.write_paged(kv_ref.as_u16(vp).copy(), kv_ref.as_u16(v),
+                                None, pos.numpy(), table.numpy())
+    kd, vd = kp.to(dev), vp.to(dev)
+    tm.kv_write_paged(k.to(dev), v.to(dev), table.to(dev), pos.to(dev), kd, vd)
+    torch.cuda.synchronize()
+    assert np.array_equal(kv_ref.as_u16(kd), want_k)
+    assert np.array_equal(kv_ref.as_u16(vd), want_v)
+
+
+def test_t_b3_paged_pin(tm, dev):
+    """t_b3.py:119-130: page size 4, shuffled free order of 8 pages, appends
+    of 5 then 8 tokens; gather reproduces logical order through a table
+    that equals order[:4]."""
+    g = torch.Generator().manual_seed(1)
+    H, D = 2, 8
+    ks = _bf16((13, H, D), g)
+    vs = _bf16((13, H, D), g)
+    order = torch.randperm(8, generator=g)
+    table = order[:4].to(torch.int32)[None].contiguous()
+    kp = torch.zeros((8, 4, H, D), dtype=torch.bfloat16, device=dev)
+    vp = torch.zeros_like(kp)
+    for s0, s1 in ((0, 5), (5, 13)):
+        tm.kv_write_paged(
+            ks[s0:s1].to(dev), vs[s0:s1].to(dev), table.to(dev),
+            torch.tensor([s0], dtype=torch.int32, device=dev), kp, vp,
+            cu_seqlens=torch.tensor([0, s1 - s0], dtype=torch.int32,
+                                    device=dev))
+    torch.cuda.synchronize()
+    got_k = kv_ref.gather(kv_ref.as_u16(kp), table[0].numpy(), 13, page=4)
+    got_v = kv_ref.gather(kv_ref.as_u16(vp), table[0].numpy(), 13, page=4)
+    assert np.array_equal(got_k, kv_ref.as_u16(ks))
+    assert np.array_equal(got_v, kv_ref.as_u16(vs))
+
+
+def test_t_b3_ring_pin(tm, dev):
+    """t_b3.py:100-117: ring capacity 8 (2 pages of 4), 13 tokens appended
+    as 3 then 10 (oversized mid-stream) or 13 at once: the live window is
+    tokens 5..12 in either case."""
+    g = torch.Generator().manual_seed(2)
+    H, D = 2, 8
+    ks = _bf16((13, H, D), g)
+    vs = _bf16((13, H, D), g)
+    table = torch.tensor([[6, 2]], dtype=torch.int32, device=dev)
+    for chunks in (((0, 3), (3, 13)), ((0, 13),)):
+        kp = torch.zeros((8, 4, H, D), dtype=torch.bfloat16, device=dev)
+        vp = torch.zeros_like(kp)
+        for s0, s1 in chunks:
+            tm.kv_write_paged(
+                ks[s0:s1].to(dev), vs[s0:s1].to(dev), table,
+                torch.tensor([s0], dtype=torch.int32, device=dev), kp, vp,
+                cu_seqlens=torch.tensor([0, s1 - s0], dtype=torch.int32,
+                                        device=dev), table_wrap=2)
+        torch.cuda.synchronize()
+        got = kv_ref.gather(kv_ref.as_u16(kp), [6, 2], 13, page=4,
+                            table_wrap=2, lo=5)
+        assert np.array_equal(got, kv_ref.as_u16(ks[5:]))
+        got = kv_ref.gather(kv_ref.as_u16(vp), [6, 2], 13, page=4,
+                            table_wrap=2, lo=5)
+        assert np.array_equal(got, kv_ref.as_u16(vs[5:]))

@@ -1,0 +1,26 @@
+"""tm-opt paged attention, MI355X-native.
+
+Hand-written gfx950 HIP kernels behind a C ABI (include/tmopt_attn.h,
+lib/libtmopt_attn.so), reached from PyTorch-ROCm through ctypes:
+
+  attn      native entry points: kv_write_slots / kv_write_paged,
+            decode_paged (split-KV + LSE combine), prefill_varlen (MFMA).
+  compat    the reference's call signatures (attn_swa, attn_global,
+            attn_prefill_fused) over the native kernels.
+  graph     hipGraph capture of the decode step.
+  workloads seeded synthetic inputs of the benchmark configurations.
+
+The directory name is not a Python identifier; import it with
+importlib.import_module("tm-opt_amd").
+"""
+from . import _lib
+from ._lib import TmoptError, TmoptLibraryMissing, version
+from .attn import (HEAD_DIM, PAGE_SIZE, decode_paged, decode_workspace_size,
+                   kv_write_paged, kv_write_slots, prefill_varlen,
+                   splits_for)
+
+__all__ = [
+    "TmoptError", "TmoptLibraryMissing", "version", "HEAD_DIM", "PAGE_SIZE",
+    "decode_paged", "decode_workspace_size", "kv_write_paged",
+    "kv_write_slots", "prefill_varlen", "splits_for",
+]

@@ -1,0 +1,219 @@
+"""Native (block-table / varlen) entry points over the C ABI.
+
+Every function here validates its tensors the way the reference wrappers do
+(dtype, shape and contiguity asserts before launch, attn_swa.py:128-132,
+attn_global.py:25-29, attn_prefill.py:169-180), then hands raw device
+pointers, sizes and strides to libtmopt_attn.so on the current stream of the
+tensors' device. Nothing here computes attention: if the library is absent
+the call raises.
+"""
+import torch
+
+from . import _lib
+
+PAGE_SIZE = 16
+HEAD_DIM = 128
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _check_rows(t, name):
+    assert t.dtype == torch.bfloat16, f"{name} must be bf16, got {t.dtype}"
+    assert t.stride(-1) == 1, f"{name}: last (head_dim) axis must be contiguous"
+
+
+# --------------------------------------------------------------------------
+# KV-cache write
+# --------------------------------------------------------------------------
+
+def kv_write_slots(k, v, slot_mapping, k_pool, v_pool):
+    """pool.view(-1, HKV, D)[slot_mapping] = k (and v), bit-exact.
+
+    k, v [T, HKV, D] bf16 (D contiguous); slot_mapping [T] int64 flat rows of
+    the pools, negative = skip; k_pool/v_pool [..., HKV, D] bf16 contiguous
+    (a [P, page, HKV, D] page pool or a [S, W, HKV, D] ring pool).
+    Reference: engine/pyengine/model.py:941-942, :947-948; kv.py:203-204."""
+    T, HKV, D = k.shape
+    assert v.shape == k.shape, (v.shape, k.shape)
+    _check_rows(k, "k")
+    _check_rows(v, "v")
+    assert slot_mapping.dtype == torch.int64 and slot_mapping.shape == (T,)
+    assert k_pool.is_contiguous() and v_pool.is_contiguous()
+    assert k_pool.shape == v_pool.shape and k_pool.dtype == torch.bfloat16
+    assert tuple(k_pool.shape[-2:]) == (HKV, D), (k_pool.shape, HKV, D)
+    rows = k_pool.numel() // (HKV * D)
+    dev = k.device
+    _lib.call("tmopt_kv_write_slots", _ptr(k), _ptr(v), k.stride(0),
+              k.stride(1), v.stride(0), v.stride(1), _ptr(slot_mapping), T,
+              HKV, D, _ptr(k_pool), _ptr(v_pool), rows, _stream(dev))
+
+
+def kv_write_paged(k, v, block_table, start_pos, k_pool, v_pool,
+                   cu_seqlens=None, max_seqlen=None, table_wrap=0):
+    """Append token runs through a block table (positions computed in-kernel).
+
+    k, v [T, HKV, D]; block_table [S, bt_stride] int32; start_pos [S] int32;
+    cu_seqlens [S+1] int32 or None (one token per sequence: the decode
+    step); pools [num_pages, page_size, HKV, D]. table_wrap > 0 makes each
+    table row a ring of table_wrap pages (sliding-window pools).
+    Reference: engine/pyengine/kv.py:89-103, :193-205; model.py:938-948."""
+    T, HKV, D = k.shape
+    assert v.shape == k.shape
+    _check_rows(k, "k")
+    _check_rows(v, "v")
+    assert block_table.dtype == torch.int32 and block_table.dim() == 2
+    assert block_table.stride(1) == 1
+    assert start_pos.dtype == torch.int32
+    S = start_pos.shape[0]
+    assert block_table.shape[0] >= S
+    if cu_seqlens is None:
+        assert T == S, (T, S)
+        max_seqlen = 1
+    else:
+        assert cu_seqlens.dtype == torch.int32 and cu_seqlens.shape == (S + 1,)
+        if max_seqlen is None:
+            max_seqlen = int((cu_seqlens[1:] - cu_seqlens[:-1]).max()) if S else 0
+    assert k_pool.is_contiguous() and v_pool.is_contiguous()
+    assert k_pool.shape == v_pool.shape and k_pool.dim() == 4
+    P, page_size = k_pool.shape[0], k_pool.shape[1]
+    assert tuple(k_pool.shape[2:]) == (HKV, D)
+    _lib.call("tmopt_kv_write_paged", _ptr(k), _ptr(v), k.stride(0),
+              k.stride(1), v.stride(0), v.stride(1), _ptr(cu_seqlens),
+              _ptr(start_pos), S, int(max_seqlen), _ptr(block_table),
+              block_table.stride(0), int(table_wrap), page_size, HKV, D,
+              _ptr(k_pool), _ptr(v_pool), P, _stream(k.device))
+
+
+# --------------------------------------------------------------------------
+# Paged decode
+# --------------------------------------------------------------------------
+
+def decode_workspace_size(B, HQ, max_splits, D=HEAD_DIM):
+    return int(_lib.load().tmopt_attn_decode_workspace_size(B, HQ, D,
+                                                            max_splits))
+
+
+def splits_for(max_visible_pages, split_pages):
+    """Grid width that covers a sequence of max_visible_pages pages."""
+    return max(1, -(-int(max_visible_pages) // int(split_pages)))
+
+
+def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
+                 table_wrap=0, rel=None, split_pages=16, max_splits=None,
+                 out=None, lse=None, workspace=None):
+    """Split-KV paged decode attention.
+
+    q [B, HQ, D] bf16 contiguous (query at position ctx_lens[b]-1);
+    k_pool/v_pool [num_pages, 16, HKV, D] bf16 contiguous; block_table
+    [B, bt_stride] int32; ctx_lens [B] int32; window 0 = global.
+    rel: optional [B, HQ, E] bf16 fused relative bias (attn_swa.py:97-102).
+    max_splits fixes the grid (None: from the block-table width, which
+    covers every sequence). Returns (out [B, HQ, D] bf16, lse [B, HQ] fp32).
+    Reference: engine/pyengine/kernels/attn_swa.py:49-141,
+    attn_global.py:15-38."""
+    B, HQ, D = q.shape
+    assert q.dtype == torch.bfloat16 and q.is_contiguous()
+    assert k_pool.is_contiguous() and v_pool.is_contiguous()
+    assert k_pool.dtype == torch.bfloat16 and v_pool.dtype == torch.bfloat16
+    assert k_pool.shape == v_pool.shape and k_pool.dim() == 4
+    P, page_size, HKV, Dk = k_pool.shape
+    assert Dk == D and HQ % HKV == 0, (k_pool.shape, q.shape)
+    assert block_table.dtype == torch.int32 and block_table.dim() == 2
+    assert block_table.stride(1) == 1 and block_table.shape[0] >= B
+    assert ctx_lens.dtype == torch.int32 and ctx_lens.shape == (B,)
+    if rel is not None:
+        assert rel.dtype == torch.bfloat16 and rel.is_contiguous()
+        assert rel.shape[:2] == (B, HQ), (rel.shape, B, HQ)
+    if table_wrap:
+        assert 0 < window <= table_wrap * page_size, \
+            "a ring table needs a window no wider than the ring"
+    if max_splits is None:
+        # visible pages: the whole table on global layers, at most
+        # ceil(W/16)+1 (a misaligned window straddles one more) on SWA ones
+        span = (-(-window // page_size) + 1) if window > 0 \
+            else block_table.shape[1]
+        max_splits = splits_for(span, split_pages)
+    dev = q.device
+    if out is None:
+        out = torch.empty_like(q)
+    if lse is None:
+        lse = torch.empty((B, HQ), dtype=torch.float32, device=dev)
+    need = decode_workspace_size(B, HQ, max_splits, D)
+    if need and workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    _lib.call("tmopt_attn_decode_paged", _ptr(q), _ptr(k_pool), _ptr(v_pool),
+              _ptr(block_table), block_table.stride(0), int(table_wrap),
+              _ptr(ctx_lens), B, HQ, HKV, D, page_size, P, int(window),
+              float(scale), _ptr(rel),
+              0 if rel is None else rel.shape[2], int(split_pages),
+              int(max_splits), _ptr(out), _ptr(lse), _ptr(workspace),
+              ws_bytes, _stream(dev))
+    return out, lse
+
+
+# --------------------------------------------------------------------------
+# Varlen prefill
+# --------------------------------------------------------------------------
+
+def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, max_seqlen=None,
+                   prior_lens=None, k_pool=None, v_pool=None,
+                   block_table=None, out=None, lse=None):
+    """Varlen causal (optionally windowed) prefill attention on bf16 MFMA.
+
+    q [total, HQ, D], k/v [total, HKV, D] bf16 (D contiguous, any token /
+    head strides); cu_seqlens [S+1] int32. With block_table (int32
+    [S, bt_stride]) every key, prior context included, is read from
+    k_pool/v_pool [num_pages, 16, HKV, D] and prior_lens [S] int32 gives the
+    position of each run's first query; the run's own keys must already be
+    in the pool. Returns (out [total, HQ, D] bf16, lse [HQ, total] fp32).
+    Reference: engine/pyengine/kernels/attn_prefill.py:71-194."""
+    total, HQ, D = q.shape
+    _check_rows(q, "q")
+    assert cu_seqlens.dtype == torch.int32 and cu_seqlens.dim() == 1
+    S = cu_seqlens.shape[0] - 1
+    if max_seqlen is None:
+        max_seqlen = int((cu_seqlens[1:] - cu_seqlens[:-1]).max()) if S else 0
+    paged = block_table is not None
+    if paged:
+        assert k_pool is not None and v_pool is not None
+        assert k_pool.is_contiguous() and v_pool.is_contiguous()
+        assert k_pool.shape == v_pool.shape and k_pool.dim() == 4
+        P, page_size, HKV, Dk = k_pool.shape
+        assert Dk == D
+        assert block_table.dtype == torch.int32 and block_table.stride(1) == 1
+        if prior_lens is not None:
+            assert prior_lens.dtype == torch.int32 and prior_lens.shape == (S,)
+        ks = vs = (0, 0)
+    else:
+        assert prior_lens is None, "prior context needs the paged source"
+        assert k is not None and v is not None
+        _check_rows(k, "k")
+        _check_rows(v, "v")
+        assert k.shape[0] == total and v.shape == k.shape and k.shape[2] == D
+        HKV = k.shape[1]
+        P, page_size = 0, PAGE_SIZE
+        ks = (k.stride(0), k.stride(1))
+        vs = (v.stride(0), v.stride(1))
+    assert HQ % HKV == 0
+    dev = q.device
+    if out is None:
+        out = torch.empty((total, HQ, D), dtype=torch.bfloat16, device=dev)
+    if lse is None:
+        lse = torch.empty((HQ, total), dtype=torch.float32, device=dev)
+    _lib.call("tmopt_attn_prefill_varlen", _ptr(q), q.stride(0), q.stride(1),
+              None if paged else _ptr(k), ks[0], ks[1],
+              None if paged else _ptr(v), vs[0], vs[1], _ptr(cu_seqlens),
+              _ptr(prior_lens), S, int(max_seqlen),
+              _ptr(k_pool) if paged else None,
+              _ptr(v_pool) if paged else None, _ptr(block_table),
+              block_table.stride(0) if paged else 0, page_size, P, HQ, HKV,
+              D, int(window), float(scale), _ptr(out), out.stride(0),
+              out.stride(1), _ptr(lse), _stream(dev))
+    return out, lse

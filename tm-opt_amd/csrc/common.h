@@ -1,0 +1,76 @@
+// Shared device/host helpers for the gfx950 paged-attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/tmopt_attn.h"
+
+namespace tmopt {
+
+// ---- vector types (clang ext_vector_type, as the MFMA builtins expect) ----
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---- bf16 bit helpers ----------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b16) {
+  return __builtin_bit_cast(float, b16 << 16);
+}
+
+// fp32 -> bf16 round-to-nearest-even (NaN kept quiet), as bits.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)f);
+}
+
+// pack two bf16 bit patterns (lo, hi) into one dword
+__device__ __forceinline__ uint32_t pack_bf16x2(uint32_t lo, uint32_t hi) {
+  return (lo & 0xffffu) | (hi << 16);
+}
+
+// Interleave the low (sel=0) or high (sel=1) bf16 halves of two dwords:
+// result = { a.half[sel], b.half[sel] }.
+__device__ __forceinline__ uint32_t interleave_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t interleave_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) {
+  return __builtin_amdgcn_exp2f(x);
+}
+__device__ __forceinline__ float fast_log2(float x) {
+  return __builtin_amdgcn_logf(x);
+}
+
+// Order LDS accesses of one wave: every lane's prior LDS writes are visible
+// to every lane's later LDS reads, and the compiler may not move LDS traffic
+// across this point.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ---- error reporting (host) ----------------------------------------------
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+int check_launch(const char* what);
+
+}  // namespace tmopt
+
+#define TMOPT_REQUIRE(cond, code, ...)      \
+  do {                                      \
+    if (!(cond)) {                          \
+      ::tmopt::set_error(__VA_ARGS__);      \
+      return (code);                        \
+    }                                       \
+  } while (0)

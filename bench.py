@@ -1,0 +1,191 @@
+"""Benchmark of the MI355X paged-attention path (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+
+A step is one pass of the hot path over one batch of synthetic input. The
+headline workload is BASELINE config 2 (global paged decode, B=64, 32Q/4KV,
+hd128, ctx U[1024, 8192], shuffled pool): one step = one decode-attention
+call over the whole batch, inputs resident in HBM. Two pool sets rotate so
+that consecutive steps never re-read the same bytes from the 256 MB
+Infinity Cache. value = algorithmic bytes of the K timed steps / their wall
+time; roofline.achieved = algorithmic bytes per launch / the launch's mean
+duration from HIP events on the launch stream.
+
+Secondary lines in "extra": config 3 (window-4096 decode), config 4 (varlen
+prefill, global and window 4096) and the KV-cache write, each with its own
+roofline fraction. The CPU baseline is the fp32 torch oracle on the host
+cores, on a bounded sample of the config-2 batch.
+
+Prints ONE JSON line.
+"""
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+
+
+def _metric():
+    with open(os.path.join(ROOT, "BASELINE.json")) as f:
+        return json.load(f)["metric"]
+
+
+def time_launches(fn, sets, steps, warmup):
+    """Warm up, then time exactly `steps` launches (rotating input sets):
+    returns (wall seconds for the timed steps, list of per-launch ms from
+    HIP events recorded on the launch stream)."""
+    for i in range(warmup):
+        fn(sets[i % len(sets)])
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record()
+        fn(sets[i % len(sets)])
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall, [a.elapsed_time(b) for a, b in ev]
+
+
+def bench_decode(tm, wl, make, steps, warmup, n_sets=2, min_pages=8,
+                 num_workgroups=0):
+    sets = [make(device="cuda", poison=False) for _ in range(n_sets)]
+    c0 = sets[0]
+    # same seed, so every set holds the same values at different addresses:
+    # rotating them keeps consecutive steps from hitting the Infinity Cache
+    bufs = {}
+    for c in sets:
+        out = torch.empty_like(c.q)
+        lse = torch.empty(c.q.shape[:2], dtype=torch.float32, device="cuda")
+        w = tm.decode_workspace(c.B, c.q.shape[1], c.k_pool.shape[2], "cuda",
+                                num_workgroups)
+        bufs[id(c)] = (out, lse, w)
+
+    def fn(c):
+        out, lse, w = bufs[id(c)]
+        tm.decode_paged(c.q, c.k_pool, c.v_pool, c.block_table, c.ctx_lens,
+                        c.scale, window=c.window, min_pages=min_pages,
+                        num_workgroups=num_workgroups, out=out, lse=lse,
+                        workspace=w)
+
+    wall, per = time_launches(fn, sets, steps, warmup)
+    nbytes = c0.algorithmic_bytes()
+    mean_ms = sum(per) / len(per)
+    return {
+        "workload": c0.name, "B": c0.B, "window": c0.window,
+        "bytes_per_launch": nbytes, "ms_per_step": wall * 1e3 / steps,
+        "us_per_launch_events": mean_ms * 1e3,
+        "gbs_wall": nbytes * steps / wall / 1e9,
+        "gbs_events": nbytes / (mean_ms * 1e-3) / 1e9,
+        "seed": c0.meta["seed"], "min_pages": min_pages,
+        "num_workgroups": num_workgroups or
+        tm.decode_default_workgroups(c0.k_pool.shape[2]),
+    }
+
+
+def cpu_baseline_decode(wl, sample_b=8):
+    """fp32 torch oracle on the host cores over the first sample_b
+    sequences of config 2; GB/s of algorithmic bytes."""
+    from oracle import attn_ref
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    c = wl.config2(device="cpu", poison=False)
+    sel = slice(0, sample_b)
+    sub = wl.DecodeCase(c.name, c.q[sel], c.k_pool, c.v_pool,
+                        c.block_table[sel], c.ctx_lens[sel], c.window,
+                        c.scale, c.meta)
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        attn_ref.decode_paged(sub.q, sub.k_pool, sub.v_pool,
+                              sub.block_table, sub.ctx_lens, sub.scale)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times)[1]
+    return {"value": sub.algorithmic_bytes() / t / 1e9, "unit": "GB/s",
+            "cores": threads, "kind": "port",
+            "sample": f"config 2, first {sample_b} of 64 sequences "
+                      f"({int(sub.ctx_lens.sum())} keys), median of 3",
+            "seconds": t}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--min-pages", type=int, default=8)
+    ap.add_argument("--wgs", type=int, default=0)
+    ap.add_argument("--only", default="")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the paged-"
+              "attention path has no multi-GPU component here); run with "
+              "--gpus 1", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    tm = importlib.import_module("tm-opt_amd")
+    wl = importlib.import_module("tm-opt_amd.workloads")
+    tm._lib.load()
+
+    head = bench_decode(tm, wl, wl.config2, args.steps, args.warmup,
+                        min_pages=args.min_pages, num_workgroups=args.wgs)
+    print(f"[bench] C2 decode {head['us_per_launch_events']:.1f} us "
+          f"{head['gbs_events']:.0f} GB/s", file=sys.stderr, flush=True)
+    extra = {}
+    if args.only in ("", "c3"):
+        c3 = bench_decode(tm, wl, wl.config3, args.steps, args.warmup,
+                          min_pages=args.min_pages, num_workgroups=args.wgs)
+        print(f"[bench] C3 decode {c3['us_per_launch_events']:.1f} us "
+              f"{c3['gbs_events']:.0f} GB/s", file=sys.stderr, flush=True)
+        extra["C3_swa_decode"] = {**c3, "roofline_frac":
+                                  c3["gbs_events"] / HBM_PEAK_GBS}
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline_decode(wl)
+        print(f"[bench] cpu baseline {cpu['value']:.2f} GB/s on "
+              f"{cpu['cores']} threads", file=sys.stderr, flush=True)
+    line = {
+        "metric": _metric(),
+        "value": round(head["gbs_wall"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 4),
+        "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16, shuffled page pool)",
+        "config": {"workload": "C2 global paged decode, B=64, 32Q/4KV, "
+                               "hd128, page 16, ctx U[1024,8192]",
+                   "batch": 64, "min_pages": head["min_pages"],
+                   "num_workgroups": head["num_workgroups"],
+                   "seed": head["seed"]},
+        "roofline": {"bound": "hbm",
+                     "achieved": round(head["gbs_events"], 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["gbs_events"] / HBM_PEAK_GBS, 4),
+                     "traffic": None,
+                     "kernel": "decode_kernel<8,false> + decode_combine_kernel",
+                     "bytes_per_launch": head["bytes_per_launch"],
+                     "us_per_launch": round(head["us_per_launch_events"], 2)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

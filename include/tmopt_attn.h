@@ -107,10 +107,20 @@ int tmopt_kv_write_paged(const void* k, const void* v, int64_t k_stride_tok,
 /* ------------------------------------------------------------------------ */
 
 /*
- * Bytes of workspace tmopt_attn_decode_paged needs for a given launch shape.
- * max_splits = ceil(max visible pages / split_pages); see below.
+ * Work-groups tmopt_attn_decode_paged launches when num_workgroups == 0
+ * (two per compute unit of the current device, divided among the
+ * HKV / 4 head groups).
  */
-size_t tmopt_attn_decode_workspace_size(int B, int HQ, int D, int max_splits);
+int tmopt_attn_decode_default_workgroups(int HKV);
+
+/*
+ * Bytes of workspace tmopt_attn_decode_paged needs for a launch shape
+ * (num_workgroups 0 = the default above): per-piece partial results of
+ * sequences that several work-groups share, plus the split geometry the
+ * merge kernel reads. No initialisation needed.
+ */
+size_t tmopt_attn_decode_workspace_size(int B, int HQ, int HKV, int D,
+                                        int num_workgroups);
 
 /*
  * One query token per sequence against its paged KV history. Replaces
@@ -128,7 +138,8 @@ size_t tmopt_attn_decode_workspace_size(int B, int HQ, int D, int max_splits);
  *               lp % table_wrap : lp)]. Only pages holding visible keys are
  *               read; entries outside [0, num_pages) are never dereferenced
  *               (their keys count as absent).
- * ctx_lens:     [B] int32 keys in the cache including the current token.
+ * ctx_lens:     [B] int32 keys in the cache including the current token
+ *               (0 = empty: output 0, LSE -inf).
  * window:       0 = global; W > 0 = sliding window, keys k with
  *               pos - k < W only (pages wholly outside are never read).
  * scale:        softmax scale applied to q.k.
@@ -136,13 +147,19 @@ size_t tmopt_attn_decode_workspace_size(int B, int HQ, int D, int max_splits);
  *               [B, HQ, rel_extent] contiguous and the score of key k gets
  *               rel[b, h, dist] for 0 <= dist = pos - k < rel_extent, else 0
  *               (attn_swa.py:97-102).
- * split_pages:  pages per split (> 0). max_splits must be >= the number of
- *               splits any sequence needs; the grid is fixed by it, so one
- *               value per hipGraph bucket keeps captures static.
+ * min_pages:    lower bound of pages per work-group (> 0). The visible
+ *               pages of the whole batch are dealt out in equal contiguous
+ *               ranges of max(ceil(total / num_workgroups), min_pages).
+ * num_workgroups: persistent grid size (0 = default). The grid does not
+ *               depend on ctx_lens, so a captured hipGraph stays valid for
+ *               any lengths.
  * out:          [B, HQ, D] bf16; lse: [B, HQ] fp32 natural-log sum-exp of
  *               the scaled scores (may be NULL).
- * workspace:    device scratch of tmopt_attn_decode_workspace_size bytes
- *               (may be NULL when max_splits == 1).
+ * workspace:    device scratch of tmopt_attn_decode_workspace_size bytes,
+ *               16-byte aligned.
+ * Two launches on `stream`: the persistent split kernel, then the merge of
+ * sequences that were split across work-groups.
+ * B <= 8192.
  */
 int tmopt_attn_decode_paged(const void* q, const void* k_pool,
                             const void* v_pool, const int32_t* block_table,
@@ -150,7 +167,7 @@ int tmopt_attn_decode_paged(const void* q, const void* k_pool,
                             const int32_t* ctx_lens, int B, int HQ, int HKV,
                             int D, int page_size, int64_t num_pages,
                             int window, float scale, const void* rel,
-                            int rel_extent, int split_pages, int max_splits,
+                            int rel_extent, int min_pages, int num_workgroups,
                             void* out, float* lse, void* workspace,
                             size_t workspace_bytes, tmopt_stream_t stream);
 

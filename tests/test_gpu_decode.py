@@ -44,16 +44,18 @@ def test_config1_global_decode(tm, dev):
 
 
 @pytest.mark.parametrize("window", [0, 512])
-@pytest.mark.parametrize("split_pages", [1, 3, 16, 128])
-def test_edge_positions(tm, dev, window, split_pages):
+@pytest.mark.parametrize("min_pages,wgs", [(1, 0), (1, 7), (3, 64), (8, 0),
+                                           (128, 0)])
+def test_edge_positions(tm, dev, window, min_pages, wgs):
     from importlib import import_module
     wl = import_module("tm-opt_amd.workloads")
     case = wl.make_decode("edges", 7, len(EDGE_POS), 0, 0, window,
                           ctx=[p + 1 for p in EDGE_POS])
     ref_o, ref_l = _oracle(case)
-    out, lse = _run(tm, case, dev, split_pages=split_pages)
-    assert_out_close(out, ref_o, f"edges w={window} sp={split_pages}")
-    assert_lse_close(lse, ref_l, f"edges w={window} sp={split_pages}")
+    out, lse = _run(tm, case, dev, min_pages=min_pages, num_workgroups=wgs)
+    what = f"edges w={window} min_pages={min_pages} wgs={wgs}"
+    assert_out_close(out, ref_o, what)
+    assert_lse_close(lse, ref_l, what)
 
 
 @pytest.mark.parametrize("hq,hkv", [(64, 8), (64, 16), (32, 4), (16, 16),
@@ -63,7 +65,7 @@ def test_gqa_shapes(tm, dev, hq, hkv):
     wl = import_module("tm-opt_amd.workloads")
     case = wl.make_decode("gqa", 8, 6, 1, 700, 0, hq=hq, hkv=hkv)
     ref_o, ref_l = _oracle(case)
-    out, lse = _run(tm, case, dev, split_pages=8)
+    out, lse = _run(tm, case, dev, min_pages=2, num_workgroups=40)
     assert_out_close(out, ref_o, f"gqa {hq}/{hkv}")
     assert_lse_close(lse, ref_l, f"gqa {hq}/{hkv}")
 
@@ -76,7 +78,7 @@ def test_window_only_reads_window_pages(tm, dev):
     case = wl.make_decode("swa", 9, 12, 700, 5000, window=1000)
     assert (case.block_table == case.meta["pool_pages"] - 1).any()
     ref_o, ref_l = _oracle(case)
-    out, lse = _run(tm, case, dev, split_pages=5)
+    out, lse = _run(tm, case, dev, min_pages=5)
     assert_out_close(out, ref_o, "swa")
     assert_lse_close(lse, ref_l, "swa")
 
@@ -86,14 +88,14 @@ def test_split_invariance_and_determinism(tm, dev):
     wl = import_module("tm-opt_amd.workloads")
     case = wl.make_decode("inv", 10, 5, 900, 3000)
     outs = []
-    for sp in (1, 2, 7, 64, 256):
-        outs.append(_run(tm, case, dev, split_pages=sp))
-    base_o, base_l = outs[-1]          # single split per sequence
+    for mp, wgs in ((1, 512), (2, 33), (7, 0), (64, 0), (4096, 1)):
+        outs.append(_run(tm, case, dev, min_pages=mp, num_workgroups=wgs))
+    base_o, base_l = outs[-1]          # one work-group walks everything
     for o, l in outs[:-1]:
         assert (o.float() - base_o.float()).abs().max() <= 2 * 2 ** -8 * \
             base_o.float().abs().max()
         assert (l - base_l).abs().max() <= 1e-4
-    again = _run(tm, case, dev, split_pages=7)
+    again = _run(tm, case, dev, min_pages=7, num_workgroups=0)
     assert torch.equal(again[0], outs[2][0]) and torch.equal(again[1],
                                                             outs[2][1])
 
@@ -104,7 +106,7 @@ def test_zero_query_closed_form(tm, dev):
     wl = import_module("tm-opt_amd.workloads")
     case = wl.make_decode("q0", 11, 7, 1, 2000, window=333)
     case.q.zero_()
-    out, lse = _run(tm, case, dev, split_pages=4)
+    out, lse = _run(tm, case, dev, min_pages=4)
     nv = case.visible().double()
     assert torch.allclose(lse.double(), torch.log(nv)[:, None].expand_as(lse),
                           atol=1e-4, rtol=0)
@@ -133,7 +135,7 @@ def test_rel_bias_and_ring_table(tm, dev):
     out, lse = tm.decode_paged(q.to(dev), kp, vp, table.to(dev),
                                (pos + 1).to(torch.int32).to(dev), 1.0 / D,
                                window=W, table_wrap=per, rel=rel.to(dev),
-                               split_pages=8)
+                               min_pages=2)
     torch.cuda.synchronize()
     assert_out_close(out, ref_o, "ring+rel")
     assert_lse_close(lse, ref_l, "ring+rel")
@@ -147,7 +149,7 @@ def test_empty_and_zero_length(tm, dev):
     c = case.to(dev)
     c.ctx_lens[1] = 0
     out, lse = tm.decode_paged(c.q, c.k_pool, c.v_pool, c.block_table,
-                               c.ctx_lens, c.scale, split_pages=1)
+                               c.ctx_lens, c.scale, min_pages=1)
     torch.cuda.synchronize()
     assert torch.all(out[1].float() == 0)
     assert torch.all(torch.isinf(lse[1])) and torch.all(lse[1] < 0)

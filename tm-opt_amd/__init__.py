@@ -15,12 +15,13 @@ importlib.import_module("tm-opt_amd").
 """
 from . import _lib
 from ._lib import TmoptError, TmoptLibraryMissing, version
-from .attn import (HEAD_DIM, PAGE_SIZE, decode_paged, decode_workspace_size,
-                   kv_write_paged, kv_write_slots, prefill_varlen,
-                   splits_for)
+from .attn import (HEAD_DIM, PAGE_SIZE, decode_default_workgroups,
+                   decode_paged, decode_workspace, decode_workspace_size,
+                   kv_write_paged, kv_write_slots, prefill_varlen)
 
 __all__ = [
     "TmoptError", "TmoptLibraryMissing", "version", "HEAD_DIM", "PAGE_SIZE",
-    "decode_paged", "decode_workspace_size", "kv_write_paged",
-    "kv_write_slots", "prefill_varlen", "splits_for",
+    "decode_default_workgroups", "decode_paged", "decode_workspace",
+    "decode_workspace_size", "kv_write_paged", "kv_write_slots",
+    "prefill_varlen",
 ]

@@ -94,27 +94,35 @@ def kv_write_paged(k, v, block_table, start_pos, k_pool, v_pool,
 # Paged decode
 # --------------------------------------------------------------------------
 
-def decode_workspace_size(B, HQ, max_splits, D=HEAD_DIM):
-    return int(_lib.load().tmopt_attn_decode_workspace_size(B, HQ, D,
-                                                            max_splits))
+def decode_default_workgroups(HKV):
+    """Grid size the library picks when num_workgroups == 0."""
+    return int(_lib.load().tmopt_attn_decode_default_workgroups(HKV))
 
 
-def splits_for(max_visible_pages, split_pages):
-    """Grid width that covers a sequence of max_visible_pages pages."""
-    return max(1, -(-int(max_visible_pages) // int(split_pages)))
+def decode_workspace_size(B, HQ, HKV, num_workgroups=0, D=HEAD_DIM):
+    return int(_lib.load().tmopt_attn_decode_workspace_size(
+        B, HQ, HKV, D, num_workgroups))
+
+
+def decode_workspace(B, HQ, HKV, device, num_workgroups=0):
+    """Scratch for decode_paged (per-piece partials + split geometry)."""
+    n = decode_workspace_size(B, HQ, HKV, num_workgroups)
+    return torch.empty(max(n, 16), dtype=torch.uint8, device=device)
 
 
 def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
-                 table_wrap=0, rel=None, split_pages=16, max_splits=None,
+                 table_wrap=0, rel=None, min_pages=8, num_workgroups=0,
                  out=None, lse=None, workspace=None):
-    """Split-KV paged decode attention.
+    """Split-KV paged decode attention (one launch, persistent grid).
 
     q [B, HQ, D] bf16 contiguous (query at position ctx_lens[b]-1);
     k_pool/v_pool [num_pages, 16, HKV, D] bf16 contiguous; block_table
-    [B, bt_stride] int32; ctx_lens [B] int32; window 0 = global.
+    [B, bt_stride] int32; ctx_lens [B] int32; window 0 = global; table_wrap
+    > 0 = each table row is a ring of that many pages (SWA ring pools).
     rel: optional [B, HQ, E] bf16 fused relative bias (attn_swa.py:97-102).
-    max_splits fixes the grid (None: from the block-table width, which
-    covers every sequence). Returns (out [B, HQ, D] bf16, lse [B, HQ] fp32).
+    min_pages / num_workgroups: work-split knobs (see the C header).
+    workspace: from decode_workspace() (allocated and zeroed if None).
+    Returns (out [B, HQ, D] bf16, lse [B, HQ] fp32).
     Reference: engine/pyengine/kernels/attn_swa.py:49-141,
     attn_global.py:15-38."""
     B, HQ, D = q.shape
@@ -133,27 +141,20 @@ def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
     if table_wrap:
         assert 0 < window <= table_wrap * page_size, \
             "a ring table needs a window no wider than the ring"
-    if max_splits is None:
-        # visible pages: the whole table on global layers, at most
-        # ceil(W/16)+1 (a misaligned window straddles one more) on SWA ones
-        span = (-(-window // page_size) + 1) if window > 0 \
-            else block_table.shape[1]
-        max_splits = splits_for(span, split_pages)
     dev = q.device
     if out is None:
         out = torch.empty_like(q)
     if lse is None:
         lse = torch.empty((B, HQ), dtype=torch.float32, device=dev)
-    need = decode_workspace_size(B, HQ, max_splits, D)
-    if need and workspace is None:
-        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
-    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    if workspace is None:
+        workspace = decode_workspace(B, HQ, HKV, dev, num_workgroups)
+    ws_bytes = workspace.numel() * workspace.element_size()
     _lib.call("tmopt_attn_decode_paged", _ptr(q), _ptr(k_pool), _ptr(v_pool),
               _ptr(block_table), block_table.stride(0), int(table_wrap),
               _ptr(ctx_lens), B, HQ, HKV, D, page_size, P, int(window),
               float(scale), _ptr(rel),
-              0 if rel is None else rel.shape[2], int(split_pages),
-              int(max_splits), _ptr(out), _ptr(lse), _ptr(workspace),
+              0 if rel is None else rel.shape[2], int(min_pages),
+              int(num_workgroups), _ptr(out), _ptr(lse), _ptr(workspace),
               ws_bytes, _stream(dev))
     return out, lse
 

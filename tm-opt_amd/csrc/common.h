@@ -51,6 +51,16 @@ __device__ __forceinline__ float fast_log2(float x) {
   return __builtin_amdgcn_logf(x);
 }
 
+// View of read-only global memory through the constant address space: a
+// wave-uniform load through it becomes a scalar (s_load) fetch that waits on
+// lgkmcnt, so it never drains the wave's in-flight vector loads. Only for
+// buffers that no kernel of the launch writes.
+template <class T>
+__device__ __forceinline__ const __attribute__((address_space(4))) T*
+as_const(const T* p) {
+  return (const __attribute__((address_space(4))) T*)p;
+}
+
 // Order LDS accesses of one wave: every lane's prior LDS writes are visible
 // to every lane's later LDS reads, and the compiler may not move LDS traffic
 // across this point.

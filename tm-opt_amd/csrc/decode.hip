@@ -1,34 +1,43 @@
-// Split-KV paged decode attention for gfx950 (CDNA4).
+// Persistent split-KV paged decode attention for gfx950 (CDNA4).
 //
 // Replaces _attn_decode_kernel (engine/pyengine/kernels/attn_swa.py:49-117):
-// one query token per sequence against its paged K/V history, GQA group of
-// REP query heads per KV head, fp32 online softmax, probabilities rounded to
-// bf16 for the P.V product (attn_swa.py:110-112), one bf16 rounding of the
-// output. Differences from the reference kernel, all MI355X-driven:
+// one query token per sequence against its paged K/V history, a GQA group
+// of REP query heads per KV head, fp32 online softmax, probabilities rounded
+// to bf16 for the P.V product (attn_swa.py:110-112), one bf16 rounding of
+// the output. What is different, and why (MI355X):
 //
-//  * Split-KV. A work-group owns (sequence b, split s, group of 4 KV heads);
-//    a split is `split_pages` consecutive pages of the visible range. Splits
-//    of one sequence are merged by a second kernel through their log-sum-exp
-//    (decode_combine_kernel). A sequence that needs one split is finalised
-//    in place and skipped by the combine.
+//  * Balanced persistent grid. The visible pages of all sequences are laid
+//    end to end (U pages in total) and work-group i of G processes the
+//    contiguous range [i*C, (i+1)*C), C = max(ceil(U / G), min_pages). Every
+//    work-group therefore streams the same number of bytes whatever the
+//    length distribution, and the grid is fixed (G = 2 per CU), so one
+//    launch shape serves every step of a captured hipGraph.
 //  * Only pages holding visible keys are touched: [lo/16, ceil(n/16)) where
 //    lo = max(0, n - window) on sliding-window layers, 0 on global ones.
+//  * A sequence cut by work-group boundaries leaves one normalised partial
+//    (O, LSE) per piece, in slot b + i of the workspace (unique: work-groups
+//    and sequences are both in order); decode_combine_kernel then merges
+//    the pieces of each such sequence in work-group order. No atomics and no
+//    cross-work-group fences (a device-scope release/acquire pair writes
+//    back and invalidates a whole XCD L2 on MI355X), and a fixed merge
+//    order, so repeated runs are bitwise identical. A sequence that one
+//    work-group covers alone is written in place and skipped by the merge.
 //  * One wave per KV head. The four waves of a work-group read the four
 //    256-byte head slices of the same token rows, so together they stream
 //    whole 16 KB pages. K and V arrive by 16-byte buffer loads whose
-//    resource is one page: a missing page (beyond the split, or a table
-//    entry outside the pool) has zero records, so its loads return zeros
-//    without touching memory and the next step's loads are always issued
-//    ahead of the current step's math (no branch, no vmcnt(0) drain).
+//    resource is one page: a missing page (past the range, or a table entry
+//    outside the pool) has zero records, so its loads return zeros without
+//    touching memory, and the next step's loads are always issued before
+//    the current step's math (no branch around them, no vmcnt(0) drain).
 //  * Scores and P.V run on MFMA (v_mfma_f32_16x16x32_bf16). S^T = K.Q^T puts
 //    16 tokens on the M axis and the REP heads (padded to 16) on N, so each
-//    lane ends up owning 8 scores of one head: the running max needs two
-//    cross-lane steps (xor 16, xor 32) and the running sum stays lane-local
-//    until the end. P^T is then already in the B-operand layout of
+//    lane owns 8 scores of one head: the running max needs two cross-lane
+//    steps (xor 16, xor 32) and the running sum stays lane-local until the
+//    end of a piece. P^T is then already in the B-operand layout of
 //    O^T = V^T.P^T; V^T comes from a per-wave LDS tile written transposed
 //    (two tokens packed per dword).
 //
-// Memory layout per step (two pages = 32 tokens, tile t = page t):
+// Per step (two pages = 32 tokens, tile t = page t):
 //  K tile t, MFMA row r <- token 16t + r; lane (r, g) loads dims 32kk+8g..+7.
 //  V: lane (r, g) loads tokens r and 16 + r of the same dims and writes the
 //  pair (V[r][d], V[16+r][d]) as one dword at LDS column pair 2r of row d.
@@ -44,6 +53,10 @@ constexpr int kD = 128;
 constexpr int kPS = 16;                      // tokens per page
 constexpr int kVtRowBytes = 88;              // 64 B of tokens + 24 B pad
 constexpr int kVtBytes = kD * kVtRowBytes;   // per wave
+constexpr int kMaxB = 8192;                  // prefix table lives in LDS
+// cache policy of the K/V page loads: non-temporal (streamed once; the
+// measured read rate of a plain stream rises from 6.2 to 6.9 TB/s with it)
+constexpr int kStreamLoad = 2;
 
 struct DecodeArgs {
   const __bf16* q;
@@ -53,125 +66,235 @@ struct DecodeArgs {
   int64_t bt_stride;
   int table_wrap;
   const int32_t* ctx_lens;
-  int HQ, HKV;
-  int64_t num_pages;
+  int B, HQ, HKV;
+  int num_pages;     // clamped to INT32_MAX: page ids are int32
   int window;
   float scale_log2;  // scale * log2(e)
   const __bf16* rel;
   int rel_extent;
-  int split_pages;
-  int max_splits;
+  int min_pages;     // lower bound of pages per work-group
   __bf16* out;
   float* lse;
-  float* part_o;    // [B, max_splits, HQ, D]
-  float* part_lse;  // [B, max_splits, HQ]
+  float* part_o;     // [B + G, HQ, D] fp32
+  float* part_lse;   // [B + G, HQ]
+  int* geo;          // [B + 2]: C, then the page-stream prefix pref[0..B]
 };
 
-struct SeqGeom {
-  int n, lo, p_lo, p_hi, sp, nsplit;
-};
+__device__ __forceinline__ int vis_lo(int n, int window) {
+  return (window > 0 && n > window) ? n - window : 0;
+}
 
-// Visible key range and split geometry of one sequence; shared by the split
-// kernel and the combine kernel so that both agree on every split.
-__device__ __forceinline__ SeqGeom seq_geom(int n, int window,
-                                            int split_pages, int max_splits) {
-  SeqGeom g;
-  g.n = n;
-  g.lo = (window > 0 && n > window) ? n - window : 0;
-  g.p_lo = g.lo / kPS;
-  g.p_hi = (n + kPS - 1) / kPS;
-  const int npg = n > 0 ? g.p_hi - g.p_lo : 0;
-  // a sequence longer than max_splits * split_pages widens its splits, so a
-  // fixed (graph-captured) grid always covers every page
-  int sp = split_pages;
-  const int need = (npg + max_splits - 1) / max_splits;
-  if (need > sp) sp = need;
-  g.sp = sp;
-  g.nsplit = npg > 0 ? (npg + sp - 1) / sp : 0;
-  return g;
+// visible pages of a sequence holding n tokens
+__device__ __forceinline__ int vis_pages(int n, int window) {
+  if (n <= 0) return 0;
+  return (n + kPS - 1) / kPS - vis_lo(n, window) / kPS;
 }
 
 __device__ __forceinline__ int page_id(const DecodeArgs& a, int b, int lp) {
   const int idx = a.table_wrap > 0 ? lp % a.table_wrap : lp;
-  const int64_t v = a.bt[(int64_t)b * a.bt_stride + idx];
-  return (v >= 0 && v < a.num_pages) ? (int)v : -1;
+  const int v = as_const(a.bt)[(int64_t)b * a.bt_stride + idx];
+  // one unsigned 32-bit compare: stays on the scalar unit (a 64-bit signed
+  // compare would borrow VGPRs that in-flight loads may still own)
+  return (unsigned)v < (unsigned)a.num_pages ? v : -1;
 }
-
-struct StepBuf {
-  u32x4 k[2][4];  // [tile][kk]
-  u32x4 v[2][4];  // [tile][kk]
-};
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t page_rsrc(const __bf16* pool,
                                                             int phys,
                                                             int page_bytes) {
-  const char* base =
-      reinterpret_cast<const char*>(pool) +
-      (phys >= 0 ? (int64_t)phys * page_bytes : 0);
+  const char* base = reinterpret_cast<const char*>(pool) +
+                     (phys >= 0 ? (int64_t)phys * page_bytes : 0);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0,
                                            phys >= 0 ? page_bytes : 0,
                                            0x00020000);
 }
 
-// Issue the 16 buffer loads of one 32-token step.
-__device__ __forceinline__ void issue_step(StepBuf& buf, const DecodeArgs& a,
-                                           int phys0, int phys1,
-                                           int lane_off, int page_bytes) {
+// One 32-token step of the flattened page stream (wave-uniform).
+struct Step {
+  int b;       // sequence (-1: past the end of this work-group's range)
+  int n;       // its context length
+  int s0, s1;  // its first and one-past-last unit in the page stream
+  int pg;      // first logical page
+  int phys0, phys1;
+  bool last;   // last step of this piece of sequence b
+};
+
+template <bool REL>
+struct StepBuf {
+  u32x4 k[2][4];  // [tile][kk]
+  u32x4 v[2][4];
+  // raw bf16 bias bits of this lane's 8 scores, [4t + i] for token
+  // 16t + 4g + i; converted only when used, so issuing never waits
+  uint32_t rel[REL ? 8 : 1];
+};
+
+// Issue the loads of one 32-token step: 16 K/V buffer loads and, with a
+// relative bias, the 8 bias values this lane's scores need.
+template <bool REL>
+__device__ __forceinline__ void issue_step(StepBuf<REL>& buf,
+                                           const DecodeArgs& a,
+                                           const Step& st, int lane_off,
+                                           int page_bytes, int hq, bool head_ok,
+                                           int g) {
+  if constexpr (REL) {
+    // rel row of sequence b: [HQ, E] bf16; out-of-band distances (and
+    // padded heads) get an out-of-range offset, which reads as 0
+    const char* base = reinterpret_cast<const char*>(a.rel) +
+                       (st.b >= 0 ? (int64_t)st.b * a.HQ * a.rel_extent * 2 : 0);
+    __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(base), (short)0,
+        st.b >= 0 ? a.HQ * a.rel_extent * 2 : 0, 0x00020000);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int dist = (st.n - 1) - ((st.pg + t) * kPS + 4 * g + i);
+        const bool in = head_ok && dist >= 0 && dist < a.rel_extent;
+        const int off = in ? (hq * a.rel_extent + dist) * 2 : 0x7ffffff0;
+        buf.rel[4 * t + i] = __builtin_amdgcn_raw_buffer_load_b16(
+            rr, off, 0, 0);
+      }
+  }
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int phys = t == 0 ? phys0 : phys1;
+    const int phys = t == 0 ? st.phys0 : st.phys1;
     __amdgpu_buffer_rsrc_t rk = page_rsrc(a.kpool, phys, page_bytes);
     __amdgpu_buffer_rsrc_t rv = page_rsrc(a.vpool, phys, page_bytes);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       buf.k[t][kk] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, lane_off + 64 * kk,
-                                                       0, 0));
+                                                       0, kStreamLoad));
       buf.v[t][kk] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, lane_off + 64 * kk,
-                                                       0, 0));
+                                                       0, kStreamLoad));
     }
   }
 }
 
-template <int REP>
-__global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
+template <int REP, bool REL>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(REL ? 1 : 2, 2)))
+void decode_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) char smem[];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int nw = blockDim.x >> 6;
   const int r = lane & 15;  // MFMA row / column index
   const int g = lane >> 4;  // MFMA k-group
-  const int b = blockIdx.z;
-  const int s = blockIdx.x;
+  const int wg = blockIdx.x;
+  const int G = gridDim.x;
   const int kvh = blockIdx.y * nw + w;
   char* vt = smem + w * kVtBytes;
+  int* pref = reinterpret_cast<int*>(smem + nw * kVtBytes);  // [B + 1]
+  int* wsum = pref + a.B + 1;                                // [4]
 
-  const int n = a.ctx_lens[b];
-  const SeqGeom geo = seq_geom(n, a.window, a.split_pages, a.max_splits);
+  // ---- 1. prefix sums of visible pages: pref[b] = first unit of seq b ----
+  {
+    int carry = 0;
+    for (int b0 = 0; b0 < a.B; b0 += blockDim.x) {
+      const int b = b0 + threadIdx.x;
+      const int v = b < a.B ? vis_pages(as_const(a.ctx_lens)[b], a.window) : 0;
+      int x = v;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off);
+        if (lane >= off) x += y;
+      }
+      if (lane == 63) wsum[w] = x;
+      __syncthreads();
+      int before = carry;
+      for (int j = 0; j < w; ++j) before += wsum[j];
+      if (b < a.B) pref[b + 1] = before + x;
+      int tot = 0;
+      for (int j = 0; j < nw; ++j) tot += wsum[j];
+      carry += tot;
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) pref[0] = 0;
+    __syncthreads();
+  }
+  const int U = __builtin_amdgcn_readfirstlane(pref[a.B]);
+  int C = (U + G - 1) / G;
+  if (C < a.min_pages) C = a.min_pages;
+  // publish the split geometry for the combine kernel
+  if (wg == 0 && blockIdx.y == 0) {
+    for (int i = threadIdx.x; i <= a.B; i += blockDim.x) a.geo[1 + i] = pref[i];
+    if (threadIdx.x == 0) a.geo[0] = C;
+  }
+  const int u0 = min(wg * C, U);
+  const int u1 = min(u0 + C, U);
   const int hq = kvh * REP + r;  // query head owned as MFMA column r
   const bool head_ok = r < REP;
 
-  if (geo.nsplit == 0) {
-    // no visible key: output 0, lse -inf (only split 0 writes)
-    if (s == 0 && head_ok) {
-      __bf16* o = a.out + ((int64_t)b * a.HQ + hq) * kD;
+  // ---- 2. sequences with no visible key: output 0, LSE -inf -------------
+  for (int b = wg; b < a.B; b += G) {
+    if (pref[b + 1] != pref[b] || !head_ok) continue;
+    __bf16* o = a.out + ((int64_t)b * a.HQ + hq) * kD;
 #pragma unroll
-      for (int blk = 0; blk < 8; ++blk)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[16 * blk + 4 * g + i] = (__bf16)0.0f;
-      if (a.lse && g == 0) a.lse[(int64_t)b * a.HQ + hq] = -INFINITY;
-    }
-    return;
+    for (int blk = 0; blk < 8; ++blk)
+      *reinterpret_cast<u32x2*>(o + 16 * blk + 4 * g) = u32x2{0, 0};
+    if (a.lse && g == 0) a.lse[(int64_t)b * a.HQ + hq] = -INFINITY;
   }
-  if (s >= geo.nsplit) return;
-  const int pb = geo.p_lo + s * geo.sp;
-  const int pe = min(pb + geo.sp, geo.p_hi);
-  const int pos = n - 1;
+  if (u0 >= u1) return;
 
-  // Q fragment: B operand of S^T = K.Q^T (column = head r, k = dims)
-  bf16x8 qf[4];
+  // ---- 3. the step stream of [u0, u1) -----------------------------------
+  // Everything about the step stream is wave-uniform and lives in SGPRs:
+  // the LDS prefix table is read only here, by the start-up binary search;
+  // afterwards the running prefix advances from scalar loads of ctx_lens,
+  // so no per-step LDS read needs a VGPR that an in-flight load still owns.
+  int cb;  // first sequence with pref[cb + 1] > u0
   {
+    int lo = 0, hi = a.B - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (__builtin_amdgcn_readfirstlane(pref[mid + 1]) > u0) hi = mid;
+      else lo = mid + 1;
+    }
+    cb = __builtin_amdgcn_readfirstlane(lo);
+  }
+  int seq_start = __builtin_amdgcn_readfirstlane(pref[cb]);
+  int cur_n = as_const(a.ctx_lens)[cb];
+  int seq_end = seq_start + vis_pages(cur_n, a.window);
+  int cu = u0;
+  auto next_step = [&](Step& st) {
+    if (cu >= u1) {
+      st.b = -1; st.n = 0; st.pg = 0; st.phys0 = -1; st.phys1 = -1;
+      st.s0 = 0; st.s1 = 0; st.last = false;
+      return;
+    }
+    while (seq_end <= cu) {
+      ++cb;
+      seq_start = seq_end;
+      cur_n = as_const(a.ctx_lens)[cb];
+      seq_end = seq_start + vis_pages(cur_n, a.window);
+    }
+    const int piece_end = min(seq_end, u1);
+    const int cnt = min(2, piece_end - cu);
+    st.b = cb;
+    st.n = cur_n;
+    st.s0 = seq_start;
+    st.s1 = seq_end;
+    st.pg = vis_lo(cur_n, a.window) / kPS + (cu - seq_start);
+    st.phys0 = page_id(a, cb, st.pg);
+    st.phys1 = cnt > 1 ? page_id(a, cb, st.pg + 1) : -1;
+    cu += cnt;
+    st.last = cu == piece_end;
+  };
+
+  const int row_elems = a.HKV * kD;
+  const int page_bytes = kPS * row_elems * 2;
+  // byte offset of (token r, head kvh, dims 8g..) inside a page
+  const int lane_off = (r * row_elems + kvh * kD + 8 * g) * 2;
+
+  // ---- per-piece state ----------------------------------------------------
+  f32x4 o_acc[8];
+#pragma unroll
+  for (int blk = 0; blk < 8; ++blk) o_acc[blk] = f32x4{0, 0, 0, 0};
+  float m_run = -INFINITY;
+  float l_part = 0.0f;
+  bf16x8 qf[4];
+  int q_b = -1;
+
+  auto load_q = [&](int b) {
     const __bf16* qrow = a.q + ((int64_t)b * a.HQ + (head_ok ? hq : 0)) * kD;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
@@ -179,24 +302,13 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
       if (!head_ok) x = u32x4{0, 0, 0, 0};
       qf[kk] = __builtin_bit_cast(bf16x8, x);
     }
-  }
+    q_b = b;
+  };
 
-  const int row_elems = a.HKV * kD;
-  const int page_bytes = kPS * row_elems * 2;
-  // byte offset of (token r, head kvh, dims 8g..) inside a page
-  const int lane_off = (r * row_elems + kvh * kD + 8 * g) * 2;
-
-  f32x4 o_acc[8];
-#pragma unroll
-  for (int blk = 0; blk < 8; ++blk) o_acc[blk] = f32x4{0, 0, 0, 0};
-  float m_run = -INFINITY;
-  float l_part = 0.0f;
-
-  const __bf16* relrow =
-      a.rel ? a.rel + ((int64_t)b * a.HQ + (head_ok ? hq : 0)) * a.rel_extent
-            : nullptr;
-
-  auto compute = [&](const StepBuf& buf, int pg, int phys0, int phys1) {
+  auto compute = [&](const StepBuf<REL>& buf, const Step& st) {
+    const int n = st.n;
+    const int lo = vis_lo(n, a.window);
+    if (st.b != q_b) load_q(st.b);
     // ---- S^T = K.Q^T for the two 16-token tiles -------------------------
     f32x4 sc[2];
 #pragma unroll
@@ -208,22 +320,17 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
             __builtin_bit_cast(bf16x8, buf.k[t][kk]), qf[kk], sc[t], 0, 0, 0);
     }
     // ---- mask, bias, running max ----------------------------------------
-    // lane (r, g) holds head r, tokens 16t + 4g + i of this step
     float x[2][4];
     float mx = -INFINITY;
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-      const bool page_ok = (t == 0 ? phys0 : phys1) >= 0;
+      const bool page_ok = (t == 0 ? st.phys0 : st.phys1) >= 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int kpos = (pg + t) * kPS + 4 * g + i;
-        const bool ok = page_ok && kpos >= geo.lo && kpos < n;
+        const int kpos = (st.pg + t) * kPS + 4 * g + i;
+        const bool ok = page_ok && kpos >= lo && kpos < n;
         float v = sc[t][i] * a.scale_log2;
-        if (relrow) {
-          const int dist = pos - kpos;
-          if (dist >= 0 && dist < a.rel_extent)
-            v += (float)relrow[dist] * kLog2e;
-        }
+        if constexpr (REL) v += bf16_bits_to_f32(buf.rel[4 * t + i]) * kLog2e;
         v = ok ? v : -INFINITY;
         x[t][i] = v;
         mx = fmaxf(mx, v);
@@ -247,12 +354,12 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
       pw[i] = pack_bf16x2(f32_to_bf16_bits(p0), f32_to_bf16_bits(p1));
     }
     l_part = l_part * alpha + psum;
-    const bf16x8 pf = __builtin_bit_cast(bf16x8, u32x4{pw[0], pw[1], pw[2], pw[3]});
-    // ---- V^T into LDS (zero rows of invalid tokens: NaN-safe) -----------
-    const bool v0_ok = phys0 >= 0 && (pg * kPS + r) >= geo.lo &&
-                       (pg * kPS + r) < n;
-    const bool v1_ok = phys1 >= 0 && ((pg + 1) * kPS + r) >= geo.lo &&
-                       ((pg + 1) * kPS + r) < n;
+    const bf16x8 pf =
+        __builtin_bit_cast(bf16x8, u32x4{pw[0], pw[1], pw[2], pw[3]});
+    // ---- V^T into LDS (rows of invalid tokens zeroed: NaN-safe) ---------
+    const int k0 = st.pg * kPS + r;
+    const bool v0_ok = st.phys0 >= 0 && k0 >= lo && k0 < n;
+    const bool v1_ok = st.phys1 >= 0 && k0 + kPS >= lo && k0 + kPS < n;
     wave_lds_sync();  // previous step's V^T reads are done
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
@@ -282,101 +389,165 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeArgs a) {
     }
   };
 
-  StepBuf A, B;
-  int phA0 = page_id(a, b, pb);
-  int phA1 = pb + 1 < pe ? page_id(a, b, pb + 1) : -1;
-  issue_step(A, a, phA0, phA1, lane_off, page_bytes);
-  int pg = pb;
-  while (true) {
-    const int phB0 = pg + 2 < pe ? page_id(a, b, pg + 2) : -1;
-    const int phB1 = pg + 3 < pe ? page_id(a, b, pg + 3) : -1;
-    issue_step(B, a, phB0, phB1, lane_off, page_bytes);
-    compute(A, pg, phA0, phA1);
-    pg += 2;
-    if (pg >= pe) break;
-    phA0 = pg + 2 < pe ? page_id(a, b, pg + 2) : -1;
-    phA1 = pg + 3 < pe ? page_id(a, b, pg + 3) : -1;
-    issue_step(A, a, phA0, phA1, lane_off, page_bytes);
-    compute(B, pg, phB0, phB1);
-    pg += 2;
-    if (pg >= pe) break;
-  }
-
-  // ---- finalise: total l over the 4 k-groups, normalise, store ----------
-  float l_tot = l_part;
-  l_tot += __shfl_xor(l_tot, 16);
-  l_tot += __shfl_xor(l_tot, 32);
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  const float lse_nat =
-      l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : -INFINITY;
-  if (!head_ok) return;
-  if (geo.nsplit == 1) {
-    __bf16* o = a.out + ((int64_t)b * a.HQ + hq) * kD;
+  // End of a piece of sequence b: write the result (whole sequence) or a
+  // normalised partial that decode_combine_kernel merges.
+  auto finish_piece = [&](const Step& st) {
+    const int b = st.b;
+    float l_tot = l_part;
+    l_tot += __shfl_xor(l_tot, 16);
+    l_tot += __shfl_xor(l_tot, 32);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    const float lse_nat =
+        l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : -INFINITY;
+    const int s0 = st.s0, s1 = st.s1;
+    if (s0 >= u0 && s1 <= u1) {
+      if (head_ok) {
+        __bf16* o = a.out + ((int64_t)b * a.HQ + hq) * kD;
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk) {
-      const uint32_t w0 = pack_bf16x2(f32_to_bf16_bits(o_acc[blk][0] * inv),
-                                      f32_to_bf16_bits(o_acc[blk][1] * inv));
-      const uint32_t w1 = pack_bf16x2(f32_to_bf16_bits(o_acc[blk][2] * inv),
-                                      f32_to_bf16_bits(o_acc[blk][3] * inv));
-      *reinterpret_cast<u32x2*>(o + 16 * blk + 4 * g) = u32x2{w0, w1};
+        for (int blk = 0; blk < 8; ++blk) {
+          const uint32_t w0 =
+              pack_bf16x2(f32_to_bf16_bits(o_acc[blk][0] * inv),
+                          f32_to_bf16_bits(o_acc[blk][1] * inv));
+          const uint32_t w1 =
+              pack_bf16x2(f32_to_bf16_bits(o_acc[blk][2] * inv),
+                          f32_to_bf16_bits(o_acc[blk][3] * inv));
+          *reinterpret_cast<u32x2*>(o + 16 * blk + 4 * g) = u32x2{w0, w1};
+        }
+        if (a.lse && g == 0) a.lse[(int64_t)b * a.HQ + hq] = lse_nat;
+      }
+    } else if (head_ok) {
+      // one piece of a longer sequence: slot b + wg is unique because
+      // work-groups and sequences are both laid out in order
+      const int64_t slot = (int64_t)(b + wg) * a.HQ + hq;
+      float* po = a.part_o + slot * kD;
+#pragma unroll
+      for (int blk = 0; blk < 8; ++blk)
+        *reinterpret_cast<f32x4*>(po + 16 * blk + 4 * g) = o_acc[blk] * inv;
+      if (g == 0) a.part_lse[slot] = lse_nat;
     }
-    if (a.lse && g == 0) a.lse[(int64_t)b * a.HQ + hq] = lse_nat;
-  } else {
-    const int64_t slot = ((int64_t)b * a.max_splits + s) * a.HQ + hq;
-    float* po = a.part_o + slot * kD;
 #pragma unroll
-    for (int blk = 0; blk < 8; ++blk)
-      *reinterpret_cast<f32x4*>(po + 16 * blk + 4 * g) = o_acc[blk] * inv;
-    if (g == 0) a.part_lse[slot] = lse_nat;
+    for (int blk = 0; blk < 8; ++blk) o_acc[blk] = f32x4{0, 0, 0, 0};
+    m_run = -INFINITY;
+    l_part = 0.0f;
+  };
+
+  // ---- 4. software-pipelined walk: next step's loads fly during math ----
+  StepBuf<REL> A, B;
+  Step sa, sb;
+  next_step(sa);
+  issue_step<REL>(A, a, sa, lane_off, page_bytes, hq, head_ok, g);
+  while (true) {
+    next_step(sb);
+    issue_step<REL>(B, a, sb, lane_off, page_bytes, hq, head_ok, g);
+    compute(A, sa);
+    if (sa.last) finish_piece(sa);
+    if (sb.b < 0) break;
+    next_step(sa);
+    issue_step<REL>(A, a, sa, lane_off, page_bytes, hq, head_ok, g);
+    compute(B, sb);
+    if (sb.last) finish_piece(sb);
+    if (sa.b < 0) break;
   }
 }
 
-// Merge the splits of every multi-split sequence: one wave per query head,
-// two dims per lane. Fixed split order, so the result is deterministic.
+// Merge the pieces of every sequence that several work-groups shared:
+// grid (B, ceil(HQ / 8)), 8 heads x 32 lanes per work-group, 4 dims per
+// lane; pieces are merged in work-group order (deterministic, no atomics),
+// four pieces' loads in flight at a time.
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
-  const int lane = threadIdx.x & 63;
-  const int hq = blockIdx.y * (blockDim.x >> 6) + (threadIdx.x >> 6);
   const int b = blockIdx.x;
-  if (hq >= a.HQ) return;
-  const SeqGeom geo =
-      seq_geom(a.ctx_lens[b], a.window, a.split_pages, a.max_splits);
-  if (geo.nsplit <= 1) return;
-  const int64_t base = (int64_t)b * a.max_splits * a.HQ + hq;
-  float m = -INFINITY;
-  for (int s = 0; s < geo.nsplit; ++s)
-    m = fmaxf(m, a.part_lse[base + (int64_t)s * a.HQ]);
-  const float m_use = m == -INFINITY ? 0.0f : m;
-  float sum = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  for (int s = 0; s < geo.nsplit; ++s) {
-    const int64_t slot = base + (int64_t)s * a.HQ;
-    const float wgt = fast_exp2((a.part_lse[slot] - m_use) * kLog2e);
-    const float2 v =
-        *reinterpret_cast<const float2*>(a.part_o + slot * kD + 2 * lane);
-    sum += wgt;
-    o0 += wgt * v.x;
-    o1 += wgt * v.y;
+  const int C = as_const(a.geo)[0];
+  const int s0 = as_const(a.geo)[1 + b];
+  const int s1 = as_const(a.geo)[2 + b];
+  if (s1 <= s0) return;                  // no visible key: written already
+  const int wfirst = s0 / C;
+  const int np = (s1 - 1) / C - wfirst + 1;
+  if (np <= 1) return;                   // one piece: written in place
+  const int h = blockIdx.y * 8 + (threadIdx.x >> 5);
+  if (h >= a.HQ) return;
+  const int d0 = 4 * (threadIdx.x & 31);
+  const int64_t slot0 = (int64_t)(b + wfirst) * a.HQ + h;
+  float m = -INFINITY, sum = 0.0f;
+  f32x4 acc = f32x4{0, 0, 0, 0};
+  for (int k = 0; k < np; k += 4) {
+    float l4[4];
+    f32x4 o4[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const bool in = k + j < np;
+      const int64_t slot = slot0 + (int64_t)(in ? k + j : 0) * a.HQ;
+      l4[j] = in ? a.part_lse[slot] : -INFINITY;
+      o4[j] = *reinterpret_cast<const f32x4*>(a.part_o + slot * kD + d0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float m_new = fmaxf(m, l4[j]);
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      const float keep = fast_exp2((m - m_use) * kLog2e);
+      const float w = fast_exp2((l4[j] - m_use) * kLog2e);
+      sum = sum * keep + w;
+      acc = acc * keep + o4[j] * w;
+      m = m_new;
+    }
   }
   const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-  __bf16* o = a.out + ((int64_t)b * a.HQ + hq) * kD + 2 * lane;
-  *reinterpret_cast<uint32_t*>(o) =
-      pack_bf16x2(f32_to_bf16_bits(o0 * inv), f32_to_bf16_bits(o1 * inv));
-  if (a.lse && lane == 0)
-    a.lse[(int64_t)b * a.HQ + hq] =
-        sum > 0.0f ? m_use + fast_log2(sum) * kLn2 : -INFINITY;
+  __bf16* o = a.out + ((int64_t)b * a.HQ + h) * kD + d0;
+  *reinterpret_cast<u32x2*>(o) =
+      u32x2{pack_bf16x2(f32_to_bf16_bits(acc[0] * inv),
+                        f32_to_bf16_bits(acc[1] * inv)),
+            pack_bf16x2(f32_to_bf16_bits(acc[2] * inv),
+                        f32_to_bf16_bits(acc[3] * inv))};
+  if (a.lse && d0 == 0)
+    a.lse[(int64_t)b * a.HQ + h] =
+        sum > 0.0f ? (m == -INFINITY ? 0.0f : m) + fast_log2(sum) * kLn2
+                   : -INFINITY;
 }
 
-size_t ws_bytes(int B, int HQ, int max_splits) {
-  if (max_splits <= 1) return 0;
-  const size_t slots = (size_t)B * max_splits * HQ;
-  const size_t o_bytes = slots * kD * sizeof(float);
-  return o_bytes + ((slots * sizeof(float) + 255) & ~(size_t)255);
+struct DeviceInfo {
+  int cus = 0;
+};
+
+int device_cus() {
+  static DeviceInfo info[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (info[dev].cus == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount,
+                              dev) != hipSuccess || n <= 0)
+      n = 256;
+    info[dev].cus = n;
+  }
+  return info[dev].cus;
+}
+
+int waves_per_wg(int HKV) { return HKV % 4 == 0 ? 4 : (HKV % 2 == 0 ? 2 : 1); }
+
+int default_wgs(int HKV) {
+  const int ny = HKV / waves_per_wg(HKV);
+  const int g = 2 * device_cus() / ny;
+  return g > 0 ? g : 1;
+}
+
+size_t ws_layout(int B, int HQ, int G, size_t* off_lse, size_t* off_geo) {
+  const size_t slots = (size_t)B + G;
+  const size_t o_bytes = slots * HQ * kD * sizeof(float);
+  const size_t l_bytes = (slots * HQ * sizeof(float) + 255) & ~(size_t)255;
+  const size_t g_bytes = (((size_t)B + 2) * sizeof(int) + 255) & ~(size_t)255;
+  if (off_lse) *off_lse = o_bytes;
+  if (off_geo) *off_geo = o_bytes + l_bytes;
+  return o_bytes + l_bytes + g_bytes;
 }
 
 template <int REP>
-void launch_split(const DecodeArgs& a, int B, int nw, hipStream_t st) {
-  dim3 grid(a.max_splits, a.HKV / nw, B);
-  hipLaunchKernelGGL(decode_split_kernel<REP>, grid, dim3(64 * nw),
-                     nw * kVtBytes, st, a);
+void launch(const DecodeArgs& a, int G, int nw, size_t lds, hipStream_t st) {
+  dim3 grid(G, a.HKV / nw);
+  if (a.rel)
+    hipLaunchKernelGGL((decode_kernel<REP, true>), grid, dim3(64 * nw), lds,
+                       st, a);
+  else
+    hipLaunchKernelGGL((decode_kernel<REP, false>), grid, dim3(64 * nw), lds,
+                       st, a);
 }
 
 }  // namespace
@@ -384,11 +555,17 @@ void launch_split(const DecodeArgs& a, int B, int nw, hipStream_t st) {
 
 using namespace tmopt;
 
-extern "C" size_t tmopt_attn_decode_workspace_size(int B, int HQ, int D,
-                                                   int max_splits) {
+extern "C" int tmopt_attn_decode_default_workgroups(int HKV) {
+  if (HKV <= 0) return 0;
+  return default_wgs(HKV);
+}
+
+extern "C" size_t tmopt_attn_decode_workspace_size(int B, int HQ, int HKV,
+                                                   int D, int num_workgroups) {
   (void)D;
-  if (B <= 0 || HQ <= 0 || max_splits <= 0) return 0;
-  return ws_bytes(B, HQ, max_splits);
+  if (B <= 0 || HQ <= 0 || HKV <= 0) return 0;
+  const int G = num_workgroups > 0 ? num_workgroups : default_wgs(HKV);
+  return ws_layout(B, HQ, G, nullptr, nullptr);
 }
 
 extern "C" int tmopt_attn_decode_paged(
@@ -396,12 +573,12 @@ extern "C" int tmopt_attn_decode_paged(
     const int32_t* block_table, int64_t bt_stride, int table_wrap,
     const int32_t* ctx_lens, int B, int HQ, int HKV, int D, int page_size,
     int64_t num_pages, int window, float scale, const void* rel,
-    int rel_extent, int split_pages, int max_splits, void* out, float* lse,
+    int rel_extent, int min_pages, int num_workgroups, void* out, float* lse,
     void* workspace, size_t workspace_bytes, tmopt_stream_t stream) {
   clear_error();
   if (B == 0) return TMOPT_OK;
-  TMOPT_REQUIRE(B > 0 && B <= 65535, TMOPT_EINVAL,
-                "decode: B=%d outside [0, 65535]", B);
+  TMOPT_REQUIRE(B > 0 && B <= kMaxB, TMOPT_EUNSUPPORTED,
+                "decode: B=%d outside [0, %d]", B, kMaxB);
   TMOPT_REQUIRE(q && k_pool && v_pool && block_table && ctx_lens && out,
                 TMOPT_EINVAL, "decode: null tensor pointer");
   TMOPT_REQUIRE(D == kD, TMOPT_EUNSUPPORTED, "decode: D=%d (only 128)", D);
@@ -421,17 +598,22 @@ extern "C" int tmopt_attn_decode_paged(
                 "decode: num_pages=%lld bt_stride=%lld table_wrap=%d",
                 (long long)num_pages, (long long)bt_stride, table_wrap);
   TMOPT_REQUIRE(window >= 0, TMOPT_EINVAL, "decode: window=%d", window);
-  TMOPT_REQUIRE(split_pages > 0 && max_splits > 0 && max_splits <= 65535,
-                TMOPT_EINVAL, "decode: split_pages=%d max_splits=%d",
-                split_pages, max_splits);
+  TMOPT_REQUIRE(min_pages > 0 && num_workgroups >= 0, TMOPT_EINVAL,
+                "decode: min_pages=%d num_workgroups=%d", min_pages,
+                num_workgroups);
   TMOPT_REQUIRE(rel == nullptr || rel_extent > 0, TMOPT_EINVAL,
                 "decode: rel_extent=%d", rel_extent);
   TMOPT_REQUIRE(((uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool |
                  (uintptr_t)out) % 16 == 0,
                 TMOPT_EINVAL, "decode: tensors must be 16-byte aligned");
-  const size_t need = ws_bytes(B, HQ, max_splits);
-  TMOPT_REQUIRE(need == 0 || (workspace && workspace_bytes >= need),
-                TMOPT_EWORKSPACE, "decode: workspace %zu bytes < %zu needed",
+  const int G = num_workgroups > 0 ? num_workgroups : default_wgs(HKV);
+  TMOPT_REQUIRE(G <= 65535, TMOPT_EINVAL, "decode: num_workgroups=%d", G);
+  size_t off_lse = 0, off_geo = 0;
+  const size_t need = ws_layout(B, HQ, G, &off_lse, &off_geo);
+  TMOPT_REQUIRE(workspace && workspace_bytes >= need &&
+                    (uintptr_t)workspace % 16 == 0,
+                TMOPT_EWORKSPACE,
+                "decode: workspace %zu bytes < %zu needed (or unaligned)",
                 workspace_bytes, need);
 
   DecodeArgs a;
@@ -442,37 +624,34 @@ extern "C" int tmopt_attn_decode_paged(
   a.bt_stride = bt_stride;
   a.table_wrap = table_wrap;
   a.ctx_lens = ctx_lens;
+  a.B = B;
   a.HQ = HQ;
   a.HKV = HKV;
-  a.num_pages = num_pages;
+  a.num_pages = num_pages > 0x7fffffff ? 0x7fffffff : (int)num_pages;
   a.window = window;
   a.scale_log2 = scale * kLog2e;
   a.rel = (const __bf16*)rel;
   a.rel_extent = rel ? rel_extent : 0;
-  a.split_pages = split_pages;
-  a.max_splits = max_splits;
+  a.min_pages = min_pages;
   a.out = (__bf16*)out;
   a.lse = lse;
-  a.part_o = need ? (float*)workspace : nullptr;
-  a.part_lse = need ? (float*)((char*)workspace +
-                               (size_t)B * max_splits * HQ * kD * sizeof(float))
-                    : nullptr;
+  a.part_o = (float*)workspace;
+  a.part_lse = (float*)((char*)workspace + off_lse);
+  a.geo = (int*)((char*)workspace + off_geo);
 
-  const int nw = HKV % 4 == 0 ? 4 : (HKV % 2 == 0 ? 2 : 1);
+  const int nw = waves_per_wg(HKV);
+  const size_t lds = (size_t)nw * kVtBytes + ((size_t)B + 1 + 4) * sizeof(int);
   hipStream_t st = (hipStream_t)stream;
   switch (rep) {
-    case 1: launch_split<1>(a, B, nw, st); break;
-    case 2: launch_split<2>(a, B, nw, st); break;
-    case 4: launch_split<4>(a, B, nw, st); break;
-    case 8: launch_split<8>(a, B, nw, st); break;
-    default: launch_split<16>(a, B, nw, st); break;
+    case 1: launch<1>(a, G, nw, lds, st); break;
+    case 2: launch<2>(a, G, nw, lds, st); break;
+    case 4: launch<4>(a, G, nw, lds, st); break;
+    case 8: launch<8>(a, G, nw, lds, st); break;
+    default: launch<16>(a, G, nw, lds, st); break;
   }
-  int rc = check_launch("decode_split");
+  int rc = check_launch("decode");
   if (rc) return rc;
-  if (max_splits > 1) {
-    dim3 grid(B, (HQ + 3) / 4);
-    hipLaunchKernelGGL(decode_combine_kernel, grid, dim3(256), 0, st, a);
-    rc = check_launch("decode_combine");
-  }
-  return rc;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(B, (HQ + 7) / 8), dim3(256),
+                     0, st, a);
+  return check_launch("decode_combine");
 }

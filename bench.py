@@ -95,6 +95,36 @@ def bench_decode(tm, wl, make, steps, warmup, n_sets=2, min_pages=8,
     }
 
 
+def bench_prefill(tm, wl, window, steps, warmup, n_sets=2):
+    """Config 4: varlen causal prefill, 8 runs T ~ U[512, 8192], once global
+    and once with window 4096. FLOPs = 4 * D * HQ * visible (q, k) pairs."""
+    sets = [wl.config4(window=window, device="cuda") for _ in range(n_sets)]
+    c0 = sets[0]
+    total = c0.q.shape[0]
+    bufs = {id(c): (torch.empty_like(c.q),
+                    torch.empty((c.q.shape[1], total), dtype=torch.float32,
+                                device="cuda")) for c in sets}
+    max_len = max(c0.lens)
+
+    def fn(c):
+        out, lse = bufs[id(c)]
+        tm.prefill_varlen(c.q, c.k, c.v, c.cu_seqlens, c.scale,
+                          window=c.window, max_seqlen=max_len, out=out,
+                          lse=lse)
+
+    wall, per = time_launches(fn, sets, steps, warmup)
+    flops = c0.algorithmic_flops()
+    mean_ms = sum(per) / len(per)
+    return {
+        "workload": c0.name, "lens": c0.lens, "window": window,
+        "flops_per_launch": flops, "ms_per_step": wall * 1e3 / steps,
+        "us_per_launch_events": mean_ms * 1e3,
+        "tflops_events": flops / (mean_ms * 1e-3) / 1e12,
+        "roofline_frac": flops / (mean_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+        "seed": c0.meta["seed"],
+    }
+
+
 def cpu_baseline_decode(wl, sample_b=8):
     """fp32 torch oracle on the host cores over the first sample_b
     sequences of config 2; GB/s of algorithmic bytes."""
@@ -154,6 +184,14 @@ def main():
               f"{c3['gbs_events']:.0f} GB/s", file=sys.stderr, flush=True)
         extra["C3_swa_decode"] = {**c3, "roofline_frac":
                                   c3["gbs_events"] / HBM_PEAK_GBS}
+    if args.only in ("", "c4"):
+        for win in (0, 4096):
+            r = bench_prefill(tm, wl, win, max(5, args.steps // 5),
+                              max(2, args.warmup // 5))
+            print(f"[bench] C4 prefill w={win} {r['us_per_launch_events']:.0f}"
+                  f" us {r['tflops_events']:.0f} TFLOP/s", file=sys.stderr,
+                  flush=True)
+            extra["C4_prefill_" + ("global" if win == 0 else f"swa{win}")] = r
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline_decode(wl)

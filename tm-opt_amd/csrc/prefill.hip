@@ -1,12 +1,411 @@
-// Varlen causal prefill attention (bf16 MFMA) — entry point placeholder
-// until the kernel lands; reports TMOPT_EUNSUPPORTED.
+// Varlen causal (optionally windowed) prefill attention on bf16 MFMA, gfx950.
+//
+// Replaces _attn_prefill_kernel (engine/pyengine/kernels/attn_prefill.py:
+// 71-141): per tile the math is the reference's — score = q.k * scale,
+// masked by causality (and the window on SWA layers) as a selection, fp32
+// online softmax, probabilities rounded to bf16 for the P.V product
+// (attn_prefill.py:134-135), fp32 accumulation, one bf16 rounding on store.
+// What is different, and why (MI355X):
+//
+//  * Packed varlen runs (cu_seqlens) instead of a right-padded [B,H,T,D]
+//    batch, and chunked prefill: query j of run i sits at position
+//    prior_i + j, and the keys may come from the paged cache through the
+//    block table (prior context + the run's own, already written, keys).
+//  * GQA grouping. A work-group owns (run, KV head, block of 256/REP
+//    queries) for all REP query heads of that KV head, i.e. 256 score rows:
+//    every K/V tile staged in LDS is used by REP heads. Each of the 8 waves
+//    owns one 32-row MFMA block (one head x 32 queries); about 200
+//    registers per wave leave room for two waves per SIMD, so one wave's
+//    MFMAs overlap the other's softmax.
+//  * Transposed scores. S^T = K.Q^T (v_mfma_f32_32x32x16_bf16, keys on M,
+//    queries on N) leaves one query per lane, so the running max needs one
+//    cross-lane step (xor 32) and the running sum stays lane-local; P^T is
+//    then already the B operand of O^T = V^T.P^T, and the rescale factor of
+//    every O^T element a lane holds is that lane's own.
+//  * K tiles are stored row-major in LDS (272-byte rows: conflict-free
+//    16-byte fragment reads); V tiles are stored transposed, each thread
+//    packing 2 keys of one dimension into one 4-byte write, with the keys
+//    of a row permuted so that every P.V fragment is one 16-byte read, and
+//    the 16-byte chunks XOR-swizzled by row group to spread the writes over
+//    the banks. Tiles are double-buffered: the next tile's global loads fly
+//    while the current tile's MFMAs run; one barrier per tile.
+//  * Tiles wholly outside the causal/window band are never visited; only
+//    tiles that straddle the diagonal, the window start or the run end pay
+//    for per-element masking.
+//  * Grid (HKV, runs, query blocks) with the query-block index reversed, so
+//    the hardware dispatches the heaviest blocks (most keys) first, level by
+//    level, and the light ones fill the tail.
 #include "common.h"
 
+namespace tmopt {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kBN = 64;                   // keys per tile
+constexpr int kKRow = 272;                // K tile row: 256 B + 16 B pad
+constexpr int kVRow = 144;                // V^T tile row: 128 B + 16 B pad
+constexpr int kKBytes = kBN * kKRow;      // 17408
+constexpr int kVBytes = kD * kVRow;       // 18432
+constexpr int kStage = kKBytes + kVBytes; // 35840; two stages per block
+
+struct PrefillArgs {
+  const __bf16* q;
+  int64_t q_st, q_sh;
+  const __bf16* k;
+  int64_t k_st, k_sh;
+  const __bf16* v;
+  int64_t v_st, v_sh;
+  const int32_t* cu;
+  const int32_t* prior;
+  const __bf16* kpool;
+  const __bf16* vpool;
+  const int32_t* bt;
+  int64_t bt_stride;
+  int num_pages;
+  int page_size;
+  int HQ, HKV;
+  int window;
+  float scale_log2;
+  __bf16* out;
+  int64_t o_st, o_sh;
+  float* lse;        // [HQ, cu[S]]
+  int S;
+};
+
+// LDS column of key kappa (0..63) in a V^T row: within each 16-key chunk the
+// keys 4a+c go to 8*(a&1) + 4*(a>>1) + c, so that lane half h of the P.V
+// MFMA finds its eight keys {4h+c, 8+4h+c} in columns 8h..8h+7.
+__device__ __forceinline__ int vt_col(int kappa) {
+  const int o = kappa & 15;
+  return (kappa & ~15) + 8 * ((o >> 2) & 1) + 4 * (o >> 3) + (o & 3);
+}
+
+// byte offset of (row d, logical 16-byte chunk ch, byte-in-chunk b) in V^T
+__device__ __forceinline__ int vt_off(int d, int ch, int b) {
+  return d * kVRow + ((ch ^ ((d >> 3) & 7)) << 4) + b;
+}
+
+template <int REP>
+__global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
+  constexpr int BQ = 256 / REP;   // queries per work-group
+  constexpr int QSUB = BQ / 32;   // 32-query sub-blocks per head
+  extern __shared__ __align__(16) char smem[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;         // 8 waves: one 32-row block each
+  const int l32 = lane & 31;
+  const int h2 = lane >> 5;       // lane half
+  const int kvh = blockIdx.x;
+  const int seq = blockIdx.y;
+  const int qb = gridDim.z - 1 - blockIdx.z;
+
+  const int t0 = as_const(a.cu)[seq];
+  const int len = as_const(a.cu)[seq + 1] - t0;
+  const int q0 = qb * BQ;
+  if (q0 >= len) return;
+  const int prior = a.prior ? as_const(a.prior)[seq] : 0;
+  const int nk = prior + len;                 // keys of this run
+  const int qn = min(BQ, len - q0);
+  const int pos_lo = prior + q0;              // first query position
+  const int pos_hi = prior + q0 + qn - 1;     // last valid query position
+  int k_lo = a.window > 0 ? max(0, pos_lo - a.window + 1) : 0;
+  k_lo = (k_lo / kBN) * kBN;
+  const int k_hi = pos_hi + 1;                // exclusive
+  const int ntiles = (k_hi - k_lo + kBN - 1) / kBN;
+  const bool paged = a.bt != nullptr;
+
+  // ---- this wave's row block: head and 32-query sub-block ----------------
+  const int head = kvh * REP + w / QSUB;
+  const int qi = q0 + 32 * (w % QSUB) + l32;  // this lane's query (column)
+  const bool qok = qi < len;
+  const int qpos = prior + qi;
+
+  // ---- Q fragments: B operand of S^T (column = query, k = dims) --------
+  bf16x8 qf[8];
+  {
+    const __bf16* row = a.q + (int64_t)(t0 + (qok ? qi : 0)) * a.q_st +
+                        (int64_t)head * a.q_sh;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      u32x4 x = *reinterpret_cast<const u32x4*>(row + 16 * kk + 8 * h2);
+      if (!qok) x = u32x4{0, 0, 0, 0};
+      qf[kk] = __builtin_bit_cast(bf16x8, x);
+    }
+  }
+
+  // ---- tile loaders (global -> registers -> LDS) -------------------------
+  // K: thread t stages keys (t>>4) + 32i (i = 0, 1), 16-byte chunk t & 15.
+  // V: thread t stages keys 2*(t>>4) + i (i = 0, 1), dims 8*(t & 15)..+7.
+  const int kc = tid & 15;
+  const int kr = tid >> 4;                    // 0..31
+  u32x4 kreg[2], vreg[2];
+
+  auto key_row = [&](int kappa, const __bf16* packed, int64_t st, int64_t sh,
+                     const __bf16* pool, bool& ok) -> const __bf16* {
+    ok = kappa < nk;
+    const int kk = ok ? kappa : 0;
+    if (paged) {
+      int pg = as_const(a.bt)[(int64_t)seq * a.bt_stride + kk / a.page_size];
+      if ((unsigned)pg >= (unsigned)a.num_pages) { ok = false; pg = 0; }
+      const int64_t row = (int64_t)pg * a.page_size + kk % a.page_size;
+      return pool + (row * a.HKV + kvh) * kD;
+    }
+    return packed + (int64_t)(t0 + kk) * st + (int64_t)kvh * sh;
+  };
+
+  auto load_tile = [&](int kt) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      bool ok;
+      const __bf16* src = key_row(kt + kr + 32 * i, a.k, a.k_st, a.k_sh,
+                                  a.kpool, ok);
+      const u32x4 x = *reinterpret_cast<const u32x4*>(src + 8 * kc);
+      kreg[i] = ok ? x : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      bool ok;
+      const __bf16* src = key_row(kt + 2 * kr + i, a.v, a.v_st, a.v_sh,
+                                  a.vpool, ok);
+      const u32x4 x = *reinterpret_cast<const u32x4*>(src + 8 * kc);
+      vreg[i] = ok ? x : u32x4{0, 0, 0, 0};
+    }
+  };
+
+  auto store_tile = [&](int stage) {
+    char* ks = smem + stage * kStage;
+    char* vs = ks + kKBytes;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      *reinterpret_cast<u32x4*>(ks + (kr + 32 * i) * kKRow + 16 * kc) =
+          kreg[i];
+    // V^T: dims 8kc+e, keys 2kr, 2kr+1 -> one 4-byte write per dim
+    const int col = vt_col(2 * kr);
+    const int ch = col >> 3;          // 16-byte chunk (8 keys)
+    const int b = (col & 7) * 2;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int d = 8 * kc + 2 * c;
+      *reinterpret_cast<uint32_t*>(vs + vt_off(d, ch, b)) =
+          interleave_lo(vreg[0][c], vreg[1][c]);
+      *reinterpret_cast<uint32_t*>(vs + vt_off(d + 1, ch, b)) =
+          interleave_hi(vreg[0][c], vreg[1][c]);
+    }
+  };
+
+  // ---- accumulators -----------------------------------------------------
+  f32x16 o_acc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) o_acc[db] = f32x16{};
+  float m_run = -INFINITY;
+  float l_part = 0.0f;
+
+  load_tile(k_lo);
+  store_tile(0);
+  __syncthreads();
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int kt = k_lo + it * kBN;
+    const int stage = it & 1;
+    if (it + 1 < ntiles) load_tile(kt + kBN);
+    const char* ks = smem + stage * kStage;
+    const char* vs = ks + kKBytes;
+
+    // does any element of this tile need masking?
+    const bool full = (kt + kBN - 1 <= pos_lo) && (kt + kBN <= nk) &&
+                      (a.window == 0 || pos_hi - kt < a.window) &&
+                      (qn == BQ);
+
+    // ---- S^T = K.Q^T ----------------------------------------------------
+    f32x16 sc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sc[kb] = f32x16{};
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const bf16x8 kf = __builtin_bit_cast(
+            bf16x8, *reinterpret_cast<const u32x4*>(
+                        ks + (32 * kb + l32) * kKRow + 32 * kk + 16 * h2));
+        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sc[kb],
+                                                         0, 0, 0);
+      }
+    }
+
+    // ---- online softmax (scores scaled / masked in place) ---------------
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        float v = sc[kb][j] * a.scale_log2;
+        if (!full) {
+          const int kp = kt + 32 * kb + 8 * (j >> 2) + 4 * h2 + (j & 3);
+          const int dist = qpos - kp;
+          const bool ok = qok && dist >= 0 && kp < nk &&
+                          (a.window == 0 || dist < a.window);
+          v = ok ? v : -INFINITY;
+        }
+        sc[kb][j] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = fast_exp2(m_run - m_use);
+    m_run = m_new;
+    float psum = 0.0f;
+    bf16x8 pf[2][2];  // [kb][kk]
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        uint32_t pw[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = fast_exp2(sc[kb][8 * kk + 2 * e] - m_use);
+          const float p1 = fast_exp2(sc[kb][8 * kk + 2 * e + 1] - m_use);
+          psum += p0 + p1;
+          pw[e] = pack_bf16x2(f32_to_bf16_bits(p0), f32_to_bf16_bits(p1));
+        }
+        pf[kb][kk] =
+            __builtin_bit_cast(bf16x8, u32x4{pw[0], pw[1], pw[2], pw[3]});
+      }
+    l_part = l_part * alpha + psum;
+    // rescale O^T only when some lane's max moved
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o_acc[db] = o_acc[db] * alpha;
+    }
+
+    // ---- O^T += V^T.P^T --------------------------------------------------
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const int d = 32 * db + l32;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const bf16x8 vf = __builtin_bit_cast(
+              bf16x8, *reinterpret_cast<const u32x4*>(
+                          vs + vt_off(d, 2 * (2 * kb + kk) + h2, 0)));
+          o_acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+              vf, pf[kb][kk], o_acc[db], 0, 0, 0);
+        }
+    }
+
+    if (it + 1 < ntiles) store_tile(stage ^ 1);
+    __syncthreads();
+  }
+
+  // ---- finalise: l over both lane halves, normalise, store --------------
+  const float l_tot = l_part + __shfl_xor(l_part, 32);
+  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  if (!qok) return;
+  __bf16* orow = a.out + (int64_t)(t0 + qi) * a.o_st + (int64_t)head * a.o_sh;
+#pragma unroll
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const uint32_t w0 = pack_bf16x2(f32_to_bf16_bits(o_acc[db][4 * g4] * inv),
+                                      f32_to_bf16_bits(o_acc[db][4 * g4 + 1] * inv));
+      const uint32_t w1 = pack_bf16x2(f32_to_bf16_bits(o_acc[db][4 * g4 + 2] * inv),
+                                      f32_to_bf16_bits(o_acc[db][4 * g4 + 3] * inv));
+      *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * g4 + 4 * h2) =
+          u32x2{w0, w1};
+    }
+  if (a.lse && h2 == 0)
+    a.lse[(int64_t)head * as_const(a.cu)[a.S] + t0 + qi] =
+        l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : -INFINITY;
+}
+
+template <int REP>
+void launch(const PrefillArgs& a, int S, int max_seqlen, hipStream_t st) {
+  constexpr int BQ = 256 / REP;
+  const int nqb = (max_seqlen + BQ - 1) / BQ;
+  dim3 grid(a.HKV, S, nqb);
+  hipLaunchKernelGGL(prefill_kernel<REP>, grid, dim3(512), 2 * kStage, st, a);
+}
+
+}  // namespace
+}  // namespace tmopt
+
+using namespace tmopt;
+
 extern "C" int tmopt_attn_prefill_varlen(
-    const void*, int64_t, int64_t, const void*, int64_t, int64_t, const void*,
-    int64_t, int64_t, const int32_t*, const int32_t*, int, int, const void*,
-    const void*, const int32_t*, int64_t, int, int64_t, int, int, int, int,
-    float, void*, int64_t, int64_t, float*, tmopt_stream_t) {
-  tmopt::set_error("prefill_varlen: not built yet");
-  return TMOPT_EUNSUPPORTED;
+    const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k,
+    int64_t k_stride_tok, int64_t k_stride_head, const void* v,
+    int64_t v_stride_tok, int64_t v_stride_head, const int32_t* cu_seqlens_q,
+    const int32_t* prior_lens, int num_seqs, int max_seqlen_q,
+    const void* k_pool, const void* v_pool, const int32_t* block_table,
+    int64_t bt_stride, int page_size, int64_t num_pages, int HQ, int HKV, int D,
+    int window, float scale, void* out, int64_t o_stride_tok,
+    int64_t o_stride_head, float* lse, tmopt_stream_t stream) {
+  clear_error();
+  if (num_seqs == 0 || max_seqlen_q == 0) return TMOPT_OK;
+  TMOPT_REQUIRE(num_seqs > 0 && num_seqs <= 65535 && max_seqlen_q > 0,
+                TMOPT_EINVAL, "prefill: num_seqs=%d max_seqlen_q=%d", num_seqs,
+                max_seqlen_q);
+  TMOPT_REQUIRE(q && out && cu_seqlens_q, TMOPT_EINVAL,
+                "prefill: null q/out/cu_seqlens");
+  TMOPT_REQUIRE(D == kD, TMOPT_EUNSUPPORTED, "prefill: D=%d (only 128)", D);
+  TMOPT_REQUIRE(HKV > 0 && HQ > 0 && HQ % HKV == 0 && HKV <= 65535,
+                TMOPT_EINVAL, "prefill: HQ=%d HKV=%d", HQ, HKV);
+  const int rep = HQ / HKV;
+  TMOPT_REQUIRE(rep == 4 || rep == 8, TMOPT_EUNSUPPORTED,
+                "prefill: HQ/HKV=%d not in {4, 8}", rep);
+  TMOPT_REQUIRE(window >= 0, TMOPT_EINVAL, "prefill: window=%d", window);
+  const bool paged = block_table != nullptr;
+  if (paged) {
+    TMOPT_REQUIRE(k_pool && v_pool && page_size > 0 && bt_stride > 0 &&
+                      num_pages > 0,
+                  TMOPT_EINVAL,
+                  "prefill: paged source needs pools, page_size, bt_stride");
+    TMOPT_REQUIRE(((uintptr_t)k_pool | (uintptr_t)v_pool) % 16 == 0,
+                  TMOPT_EINVAL, "prefill: pools must be 16-byte aligned");
+  } else {
+    TMOPT_REQUIRE(k && v && prior_lens == nullptr, TMOPT_EINVAL,
+                  "prefill: packed source needs k/v and no prior context");
+    TMOPT_REQUIRE(k_stride_tok % 8 == 0 && k_stride_head % 8 == 0 &&
+                      v_stride_tok % 8 == 0 && v_stride_head % 8 == 0 &&
+                      ((uintptr_t)k | (uintptr_t)v) % 16 == 0,
+                  TMOPT_EINVAL,
+                  "prefill: k/v rows must be 16-byte aligned (strides %% 8)");
+  }
+  TMOPT_REQUIRE(q_stride_tok % 8 == 0 && q_stride_head % 8 == 0 &&
+                    o_stride_tok % 4 == 0 && o_stride_head % 4 == 0 &&
+                    (uintptr_t)q % 16 == 0 && (uintptr_t)out % 8 == 0,
+                TMOPT_EINVAL, "prefill: q/out rows misaligned");
+  PrefillArgs a;
+  a.q = (const __bf16*)q;
+  a.q_st = q_stride_tok;
+  a.q_sh = q_stride_head;
+  a.k = (const __bf16*)k;
+  a.k_st = k_stride_tok;
+  a.k_sh = k_stride_head;
+  a.v = (const __bf16*)v;
+  a.v_st = v_stride_tok;
+  a.v_sh = v_stride_head;
+  a.cu = cu_seqlens_q;
+  a.prior = prior_lens;
+  a.kpool = (const __bf16*)k_pool;
+  a.vpool = (const __bf16*)v_pool;
+  a.bt = block_table;
+  a.bt_stride = bt_stride;
+  a.num_pages = num_pages > 0x7fffffff ? 0x7fffffff : (int)num_pages;
+  a.page_size = page_size > 0 ? page_size : 16;
+  a.HQ = HQ;
+  a.HKV = HKV;
+  a.window = window;
+  a.scale_log2 = scale * kLog2e;
+  a.out = (__bf16*)out;
+  a.o_st = o_stride_tok;
+  a.o_sh = o_stride_head;
+  a.lse = lse;
+  a.S = num_seqs;
+  hipStream_t st = (hipStream_t)stream;
+  if (rep == 8)
+    launch<8>(a, num_seqs, max_seqlen_q, st);
+  else
+    launch<4>(a, num_seqs, max_seqlen_q, st);
+  return check_launch("prefill");
 }

@@ -35,6 +35,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(uint32_t lo, uint32_t hi) {
   return (lo & 0xffffu) | (hi << 16);
 }
 
+// Two fp32 -> one dword of two bf16 (lo, hi), round-to-nearest-even, in one
+// v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2_rn(float lo, float hi) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(
+      uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+}
+
 // Interleave the low (sel=0) or high (sel=1) bf16 halves of two dwords:
 // result = { a.half[sel], b.half[sel] }.
 __device__ __forceinline__ uint32_t interleave_lo(uint32_t a, uint32_t b) {

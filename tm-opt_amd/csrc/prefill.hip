@@ -47,6 +47,7 @@ constexpr int kVRow = 144;                // V^T tile row: 128 B + 16 B pad
 constexpr int kKBytes = kBN * kKRow;      // 17408
 constexpr int kVBytes = kD * kVRow;       // 18432
 constexpr int kStage = kKBytes + kVBytes; // 35840; two stages per block
+constexpr float kLazy = 8.0f;             // lazy-rescale threshold (log2)
 
 struct PrefillArgs {
   const __bf16* q;
@@ -136,49 +137,95 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // ---- tile loaders (global -> registers -> LDS) -------------------------
   // K: thread t stages keys (t>>4) + 32i (i = 0, 1), 16-byte chunk t & 15.
   // V: thread t stages keys 2*(t>>4) + i (i = 0, 1), dims 8*(t & 15)..+7.
+  // The loads of tile j+1 are issued before tile j's math and consumed only
+  // by the LDS stores after it, so nothing may look at the loaded values in
+  // between (a select on them would make every load complete on the spot).
+  // Packed source: buffer loads over the run's rows; keys past the run fall
+  // outside the resource and read as zero. Paged source: global loads with
+  // a clamped address; the validity bits are applied at store time.
   const int kc = tid & 15;
   const int kr = tid >> 4;                    // 0..31
   u32x4 kreg[2], vreg[2];
+  unsigned okbits = 0xf;
+  // (paged launches pass no k / v: their resources are empty and unused)
+  const char* kb0 = paged ? nullptr : reinterpret_cast<const char*>(
+      a.k + (int64_t)t0 * a.k_st + (int64_t)kvh * a.k_sh);
+  const char* vb0 = paged ? nullptr : reinterpret_cast<const char*>(
+      a.v + (int64_t)t0 * a.v_st + (int64_t)kvh * a.v_sh);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(kb0), (short)0,
+      paged ? 0 : (int)(((int64_t)(len - 1) * a.k_st + kD) * 2), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(vb0), (short)0,
+      paged ? 0 : (int)(((int64_t)(len - 1) * a.v_st + kD) * 2), 0x00020000);
+  const int kst_b = (int)(a.k_st * 2), vst_b = (int)(a.v_st * 2);
+  const int koff[2] = {kr * kst_b + 16 * kc, (kr + 32) * kst_b + 16 * kc};
+  const int voff[2] = {2 * kr * vst_b + 16 * kc, (2 * kr + 1) * vst_b + 16 * kc};
 
-  auto key_row = [&](int kappa, const __bf16* packed, int64_t st, int64_t sh,
-                     const __bf16* pool, bool& ok) -> const __bf16* {
+  // page of tile-local key kl (0..63) among the tile's 4 pages, fetched
+  // once per tile with wave-uniform scalar loads (a per-lane table load
+  // would have to complete before the K/V loads it addresses)
+  const int last_lp = (nk - 1) / a.page_size;
+  auto paged_row = [&](int p0, int p1, int p2, int p3, int kt, int kl,
+                       const __bf16* pool, bool& ok) {
+    const int kappa = kt + kl;
     ok = kappa < nk;
-    const int kk = ok ? kappa : 0;
-    if (paged) {
-      int pg = as_const(a.bt)[(int64_t)seq * a.bt_stride + kk / a.page_size];
-      if ((unsigned)pg >= (unsigned)a.num_pages) { ok = false; pg = 0; }
-      const int64_t row = (int64_t)pg * a.page_size + kk % a.page_size;
-      return pool + (row * a.HKV + kvh) * kD;
-    }
-    return packed + (int64_t)(t0 + kk) * st + (int64_t)kvh * sh;
+    int pg = p0;
+    pg = (kl >> 4) == 1 ? p1 : pg;
+    pg = (kl >> 4) == 2 ? p2 : pg;
+    pg = (kl >> 4) == 3 ? p3 : pg;
+    if ((unsigned)pg >= (unsigned)a.num_pages) { ok = false; pg = 0; }
+    const int64_t row = (int64_t)pg * a.page_size + (kappa % a.page_size);
+    return pool + (row * a.HKV + kvh) * kD + 8 * kc;
   };
 
   auto load_tile = [&](int kt) {
+    if (!paged) {
+      // per-thread offsets are loop-invariant; the tile offset rides in the
+      // scalar soffset field
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      bool ok;
-      const __bf16* src = key_row(kt + kr + 32 * i, a.k, a.k_st, a.k_sh,
-                                  a.kpool, ok);
-      const u32x4 x = *reinterpret_cast<const u32x4*>(src + 8 * kc);
-      kreg[i] = ok ? x : u32x4{0, 0, 0, 0};
-    }
+      for (int i = 0; i < 2; ++i) {
+        kreg[i] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rk, koff[i], kt * kst_b, 0));
+        vreg[i] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                       rv, voff[i], kt * vst_b, 0));
+      }
+    } else {
+      const int32_t __attribute__((address_space(4)))* trow =
+          as_const(a.bt) + (int64_t)seq * a.bt_stride;
+      const int lp0 = kt / a.page_size;
+      const int p0 = trow[min(lp0, last_lp)];
+      const int p1 = trow[min(lp0 + 1, last_lp)];
+      const int p2 = trow[min(lp0 + 2, last_lp)];
+      const int p3 = trow[min(lp0 + 3, last_lp)];
+      unsigned bits = 0;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      bool ok;
-      const __bf16* src = key_row(kt + 2 * kr + i, a.v, a.v_st, a.v_sh,
-                                  a.vpool, ok);
-      const u32x4 x = *reinterpret_cast<const u32x4*>(src + 8 * kc);
-      vreg[i] = ok ? x : u32x4{0, 0, 0, 0};
+      for (int i = 0; i < 2; ++i) {
+        bool ok;
+        const __bf16* src =
+            paged_row(p0, p1, p2, p3, kt, kr + 32 * i, a.kpool, ok);
+        kreg[i] = *reinterpret_cast<const u32x4*>(src);
+        bits |= ok ? (1u << i) : 0u;
+        src = paged_row(p0, p1, p2, p3, kt, 2 * kr + i, a.vpool, ok);
+        vreg[i] = *reinterpret_cast<const u32x4*>(src);
+        bits |= ok ? (4u << i) : 0u;
+      }
+      okbits = bits;
     }
   };
 
   auto store_tile = [&](int stage) {
     char* ks = smem + stage * kStage;
     char* vs = ks + kKBytes;
+    const u32x4 z = u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       *reinterpret_cast<u32x4*>(ks + (kr + 32 * i) * kKRow + 16 * kc) =
-          kreg[i];
+          (okbits & (1u << i)) ? kreg[i] : z;
+    const u32x4 v0 = (okbits & 4u) ? vreg[0] : z;
+    const u32x4 v1 = (okbits & 8u) ? vreg[1] : z;
     // V^T: dims 8kc+e, keys 2kr, 2kr+1 -> one 4-byte write per dim
     const int col = vt_col(2 * kr);
     const int ch = col >> 3;          // 16-byte chunk (8 keys)
@@ -187,9 +234,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     for (int c = 0; c < 4; ++c) {
       const int d = 8 * kc + 2 * c;
       *reinterpret_cast<uint32_t*>(vs + vt_off(d, ch, b)) =
-          interleave_lo(vreg[0][c], vreg[1][c]);
+          interleave_lo(v0[c], v1[c]);
       *reinterpret_cast<uint32_t*>(vs + vt_off(d + 1, ch, b)) =
-          interleave_hi(vreg[0][c], vreg[1][c]);
+          interleave_hi(v0[c], v1[c]);
     }
   };
 
@@ -231,27 +278,37 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
       }
     }
 
-    // ---- online softmax (scores scaled / masked in place) ---------------
-    float mx = -INFINITY;
+    // ---- online softmax -------------------------------------------------
+    // The max runs on the raw scores (scale > 0 commutes with max); each
+    // probability is then one fma + exp2: p = 2^(s * scale*log2e - m).
+    if (!full) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        float v = sc[kb][j] * a.scale_log2;
-        if (!full) {
+        for (int j = 0; j < 16; ++j) {
           const int kp = kt + 32 * kb + 8 * (j >> 2) + 4 * h2 + (j & 3);
           const int dist = qpos - kp;
           const bool ok = qok && dist >= 0 && kp < nk &&
                           (a.window == 0 || dist < a.window);
-          v = ok ? v : -INFINITY;
+          sc[kb][j] = ok ? sc[kb][j] : -INFINITY;
         }
-        sc[kb][j] = v;
-        mx = fmaxf(mx, v);
-      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 16; j += 2)
+        mx = fmaxf(fmaxf(mx, sc[kb][j]), sc[kb][j + 1]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
+    // Lazy rescaling: the running max (log2 domain) only moves when the
+    // tile's max exceeds it by more than kLazy, so probabilities stay below
+    // 2^kLazy and O^T / l are rescaled on few tiles; O / l and the LSE are
+    // exact for any reference point.
+    const float m_cand = mx * a.scale_log2;
+    const bool move = m_cand > m_run + kLazy;
+    const float m_new = move ? m_cand : m_run;
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = fast_exp2(m_run - m_use);
+    const float alpha = move ? fast_exp2(m_run - m_use) : 1.0f;
     m_run = m_new;
     float psum = 0.0f;
     bf16x8 pf[2][2];  // [kb][kk]
@@ -262,17 +319,19 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         uint32_t pw[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float p0 = fast_exp2(sc[kb][8 * kk + 2 * e] - m_use);
-          const float p1 = fast_exp2(sc[kb][8 * kk + 2 * e + 1] - m_use);
+          const float p0 = fast_exp2(
+              __builtin_fmaf(sc[kb][8 * kk + 2 * e], a.scale_log2, -m_use));
+          const float p1 = fast_exp2(
+              __builtin_fmaf(sc[kb][8 * kk + 2 * e + 1], a.scale_log2, -m_use));
           psum += p0 + p1;
-          pw[e] = pack_bf16x2(f32_to_bf16_bits(p0), f32_to_bf16_bits(p1));
+          pw[e] = pack_bf16x2_rn(p0, p1);
         }
         pf[kb][kk] =
             __builtin_bit_cast(bf16x8, u32x4{pw[0], pw[1], pw[2], pw[3]});
       }
     l_part = l_part * alpha + psum;
-    // rescale O^T only when some lane's max moved
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+    // rescale O^T only when some lane's reference point moved
+    if (__builtin_amdgcn_ballot_w64(move)) {
 #pragma unroll
       for (int db = 0; db < 4; ++db) o_acc[db] = o_acc[db] * alpha;
     }
@@ -354,6 +413,7 @@ extern "C" int tmopt_attn_prefill_varlen(
   TMOPT_REQUIRE(rep == 4 || rep == 8, TMOPT_EUNSUPPORTED,
                 "prefill: HQ/HKV=%d not in {4, 8}", rep);
   TMOPT_REQUIRE(window >= 0, TMOPT_EINVAL, "prefill: window=%d", window);
+  TMOPT_REQUIRE(scale > 0.0f, TMOPT_EINVAL, "prefill: scale must be > 0");
   const bool paged = block_table != nullptr;
   if (paged) {
     TMOPT_REQUIRE(k_pool && v_pool && page_size > 0 && bt_stride > 0 &&
@@ -365,6 +425,12 @@ extern "C" int tmopt_attn_prefill_varlen(
   } else {
     TMOPT_REQUIRE(k && v && prior_lens == nullptr, TMOPT_EINVAL,
                   "prefill: packed source needs k/v and no prior context");
+    TMOPT_REQUIRE(((int64_t)max_seqlen_q * (k_stride_tok > v_stride_tok
+                                                ? k_stride_tok
+                                                : v_stride_tok) +
+                   kD) * 2 < (1ll << 31),
+                  TMOPT_EUNSUPPORTED,
+                  "prefill: a run's packed k/v span must stay below 2 GiB");
     TMOPT_REQUIRE(k_stride_tok % 8 == 0 && k_stride_head % 8 == 0 &&
                       v_stride_tok % 8 == 0 && v_stride_head % 8 == 0 &&
                       ((uintptr_t)k | (uintptr_t)v) % 16 == 0,

@@ -196,6 +196,11 @@ int tmopt_attn_decode_paged(const void* q, const void* k_pool,
  *         be written (tmopt_kv_write_paged), k and v are ignored.
  * window: 0 = causal; W > 0 adds pos_q - pos_k < W. Key tiles wholly
  *         outside the causal/window band are skipped.
+ * scale:  softmax scale (> 0).
+ * rel, rel_extent: optional fused relative bias (NULL = off): row r of q
+ *         (token) and head h own rel[r * rel_stride_tok + h * rel_stride_head
+ *         + dist] for 0 <= dist = pos_q - pos_k < rel_extent; pairs outside
+ *         that band get 0 (attn_prefill.py:115-120).
  * max_seqlen_q bounds every len_i (it sizes the grid).
  * out:    [total_q, HQ, D] with element strides (o_stride_tok,
  *         o_stride_head), D contiguous.
@@ -209,7 +214,8 @@ int tmopt_attn_prefill_varlen(
     const int32_t* prior_lens, int num_seqs, int max_seqlen_q,
     const void* k_pool, const void* v_pool, const int32_t* block_table,
     int64_t bt_stride, int page_size, int64_t num_pages, int HQ, int HKV, int D,
-    int window, float scale, void* out, int64_t o_stride_tok,
+    int window, float scale, const void* rel, int64_t rel_stride_tok,
+    int64_t rel_stride_head, int rel_extent, void* out, int64_t o_stride_tok,
     int64_t o_stride_head, float* lse, tmopt_stream_t stream);
 
 #ifdef __cplusplus

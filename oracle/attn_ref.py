@@ -152,3 +152,33 @@ def decode_reference_semantics(q, pool_k, pool_v, slots, pos, rel, window):
     ctx = pos.to(torch.int64) + 1
     return decode_paged(q, kp, vp, table, ctx, 1.0 / D, window=W,
                         table_wrap=per, rel=rel)
+
+
+def prefill_reference_semantics(q, k, v, rel, positions, window):
+    """attn_prefill_fused's model semantics on the padded batch
+    (engine/pyengine/kernels/attn_prefill.py:114-124, the eager chain
+    model.py:530-556 with rel_bias model.py:137-158): score = q.k / D +
+    rel[b, h, q, clamp(dist, 0, E-1)] zeroed outside 0 <= dist < E, kept
+    iff 0 <= dist (< window on SWA layers), fp32 softmax.
+    q [B, H, T, D], k/v [B, HK, T, D], rel [B, H, T, E], positions [T].
+    Returns [B, T, H, D] fp32."""
+    B, H, T, D = q.shape
+    HK = k.shape[1]
+    E = rel.shape[3]
+    rep = H // HK
+    pos = positions.to(torch.int64).cpu()
+    dist = pos[:, None] - pos[None, :]                       # [T, T]
+    idx = dist.clamp(0, E - 1)
+    band = (dist >= 0) & (dist < E)
+    keep = dist >= 0
+    if window is not None:
+        keep &= dist < window
+    kh = k.float().repeat_interleave(rep, 1)
+    vh = v.float().repeat_interleave(rep, 1)
+    s = torch.matmul(q.float(), kh.transpose(2, 3)) / D      # [B,H,T,T]
+    r = rel.float()
+    bias = torch.gather(r, 3, idx[None, None].expand(B, H, T, T))
+    s = s + torch.where(band[None, None], bias, torch.zeros(()))
+    s = s.masked_fill(~keep[None, None], -math.inf)
+    p = torch.softmax(s, -1)
+    return torch.matmul(p, vh).transpose(1, 2)

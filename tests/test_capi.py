@@ -1,0 +1,97 @@
+"""CPU checks of the C-ABI boundary: the built library loads, exports every
+entry point include/tmopt_attn.h declares, the ctypes table mirrors the
+header, and argument validation fails with a status code (no GPU needed:
+invalid calls return before any HIP call)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tmopt_attn.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tmopt_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_boundary():
+    fns = header_functions()
+    for want in ("tmopt_kv_write_slots", "tmopt_kv_write_paged",
+                 "tmopt_attn_decode_paged", "tmopt_attn_decode_workspace_size",
+                 "tmopt_attn_prefill_varlen", "tmopt_last_error"):
+        assert want in fns
+
+
+def test_library_exports_every_declared_symbol(tm):
+    lib = tm._lib.load()
+    missing = [f for f in header_functions() if not hasattr(lib, f)]
+    assert not missing, missing
+
+
+def test_ctypes_table_mirrors_header(tm):
+    assert sorted(tm._lib.SIGNATURES) == header_functions()
+
+
+def test_library_symbols_with_nm(tm):
+    """The .so's dynamic symbol table carries the C names (no mangling)."""
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", tm._lib.LIB_PATH],
+                         capture_output=True, text=True)
+    if out.returncode != 0:
+        pytest.skip("nm unavailable")
+    names = {l.split()[-1] for l in out.stdout.splitlines() if l.strip()}
+    for f in header_functions():
+        assert f in names, f
+
+
+def test_invalid_arguments_return_status(tm):
+    lib = tm._lib.load()
+    null = ctypes.c_void_p(0)
+    # decode: B < 0 is rejected before anything touches the device
+    rc = lib.tmopt_attn_decode_paged(null, null, null, null, 1, 0, null, -1,
+                                     32, 4, 128, 16, 1, 0, 0.1, null, 0, 8,
+                                     0, null, null, null, 0, null)
+    assert rc == tm._lib.TMOPT_EINVAL
+    assert b"B=-1" in lib.tmopt_last_error()
+    # decode: head_dim 64 is outside the supported set
+    p = ctypes.c_void_p(16)
+    rc = lib.tmopt_attn_decode_paged(p, p, p, p, 1, 0, p, 1, 32, 4, 64, 16,
+                                     1, 0, 0.1, null, 0, 8, 0, p, null, p,
+                                     1 << 20, null)
+    assert rc == tm._lib.TMOPT_EUNSUPPORTED
+    # prefill: REP 3 is unsupported
+    rc = lib.tmopt_attn_prefill_varlen(p, 0, 0, p, 0, 0, p, 0, 0, p, null, 1,
+                                       4, null, null, null, 0, 16, 0, 12, 4,
+                                       128, 0, 0.1, null, 0, 0, 0, p, 0, 0,
+                                       null, null)
+    assert rc == tm._lib.TMOPT_EUNSUPPORTED
+    # kv write: misaligned strides
+    rc = lib.tmopt_kv_write_slots(p, p, 3, 8, 8, 8, p, 1, 4, 128, p, p, 10,
+                                  null)
+    assert rc == tm._lib.TMOPT_EUNSUPPORTED
+    # zero-size work is a successful no-op
+    assert lib.tmopt_kv_write_slots(null, null, 0, 0, 0, 0, null, 0, 4, 128,
+                                    null, null, 0, null) == 0
+
+
+def test_python_wrapper_asserts_before_launch(tm):
+    """The reference wrappers assert dtype/contiguity before launching
+    (attn_swa.py:128-132); so do ours (no device needed to trip them)."""
+    import torch
+    q = torch.zeros((2, 32, 128), dtype=torch.float32)
+    pool = torch.zeros((4, 16, 4, 128), dtype=torch.bfloat16)
+    bt = torch.zeros((2, 4), dtype=torch.int32)
+    ctx = torch.ones(2, dtype=torch.int32)
+    with pytest.raises(AssertionError):
+        tm.decode_paged(q, pool, pool, bt, ctx, 0.1)
+    with pytest.raises(AssertionError):
+        tm.decode_paged(q.to(torch.bfloat16), pool, pool, bt.long(), ctx, 0.1)
+
+
+def test_missing_library_fails_loudly(tm, tmp_path):
+    with pytest.raises(tm.TmoptLibraryMissing):
+        tm._lib.load(str(tmp_path / "absent.so"))

@@ -1,0 +1,96 @@
+"""The reference-signature adapters (attn_swa, attn_global,
+attn_prefill_fused) against the oracle's restatement of the model
+semantics: scale 1/head_dim, fused relative bias, ring SWA pool, per-token
+`flat` rows built exactly like model.py:938-945, padded [B,H,T,D] prefill
+with channel-major K/V. Geometry edges of the reference's own arm
+(t_fused_attn.py:119-122): 0, 3, 200, 511, 512, 513, 800, 1500 and a dead
+row at position 0 on the scratch slot."""
+import pytest
+import torch
+
+from helpers import assert_out_close
+from oracle import attn_ref
+
+pytestmark = pytest.mark.gpu
+
+
+def test_attn_swa_ring_pool(tm, dev):
+    g = torch.Generator().manual_seed(13)
+    W, HK, D, HQ = 512, 16, 128, 64
+    pos = torch.tensor([0, 3, 200, 511, 512, 513, 800, 0])
+    MB = pos.shape[0]
+    # stale random bytes everywhere (dead slots must be excluded by the
+    # window, never read as zeros); shuffled slot map, scratch row last
+    pool_k = (torch.randn((MB + 1, W, HK, D), generator=g) * 0.5).to(
+        torch.bfloat16)
+    pool_v = (torch.randn((MB + 1, W, HK, D), generator=g) * 0.5).to(
+        torch.bfloat16)
+    slots = torch.cat([torch.randperm(MB - 1, generator=g),
+                       torch.tensor([MB])])
+    q = torch.randn((MB, HQ, D), generator=g).to(torch.bfloat16)
+    rel = (torch.randn((MB, HQ, W), generator=g) * 0.5).to(torch.bfloat16)
+    ref, _ = attn_ref.decode_reference_semantics(q, pool_k, pool_v, slots,
+                                                 pos, rel, W)
+    out = tm.attn_swa(q.to(dev), pool_k.to(dev), pool_v.to(dev),
+                      slots.to(dev), pos.to(dev), rel.to(dev))
+    torch.cuda.synchronize()
+    assert out.shape == (MB, HQ, D) and out.dtype == torch.bfloat16
+    assert_out_close(out, ref, "attn_swa")
+
+
+def test_attn_global_flat_rows(tm, dev):
+    g = torch.Generator().manual_seed(14)
+    HK, D, HQ, E = 8, 128, 64, 1024
+    pos_host = [0, 3, 200, 511, 512, 513, 800, 1500, 0]
+    MB = len(pos_host)
+    num_pages = (max(pos_host) + 16) // 16 + 2
+    total = MB * num_pages
+    kp = (torch.randn((total + 1, 16, HK, D), generator=g) * 0.5).to(
+        torch.bfloat16)
+    vp = (torch.randn((total + 1, 16, HK, D), generator=g) * 0.5).to(
+        torch.bfloat16)
+    table_dev = torch.zeros((MB + 1, num_pages), dtype=torch.int64)
+    table_dev[:MB] = torch.randperm(total, generator=g).view(MB, num_pages)
+    table_dev[MB] = total                                  # scratch page
+    slots = torch.cat([torch.randperm(MB - 1, generator=g),
+                       torch.tensor([MB])])
+    pos = torch.tensor(pos_host)
+    # model.py:938-945 + decode_batch_ctx #2 (model.py:849-857)
+    Lg = max(pos_host) + 1
+    j = torch.arange(Lg)
+    table = table_dev[slots]
+    flat = table[:, j // 16] * 16 + (j % 16)[None, :]
+    flat = torch.where(j[None, :] < (pos + 1)[:, None], flat,
+                       torch.zeros_like(flat))
+    q = torch.randn((MB, HQ, D), generator=g).to(torch.bfloat16)
+    rel = (torch.randn((MB, HQ, E), generator=g) * 0.5).to(torch.bfloat16)
+    ref, _ = attn_ref.decode_paged(q, kp, vp, table, pos + 1, 1.0 / D,
+                                   rel=rel)
+    out = tm.attn_global(q.to(dev), kp.to(dev), vp.to(dev),
+                         flat.contiguous().to(dev), pos.to(dev), rel.to(dev),
+                         Lg)
+    torch.cuda.synchronize()
+    assert_out_close(out, ref, "attn_global")
+
+
+@pytest.mark.parametrize("window,E", [(None, 1024), (64, 64)])
+@pytest.mark.parametrize("hq,hk", [(32, 4), (64, 16)])
+def test_attn_prefill_fused_padded_batch(tm, dev, window, E, hq, hk):
+    g = torch.Generator().manual_seed(15)
+    B, T, D = 3, 200, 128
+    q = torch.randn((B, T, hq, D), generator=g).to(torch.bfloat16).transpose(
+        1, 2)                                              # [B,H,T,D] view
+    # K/V channel-major, as the eager sconv hands them over
+    kc = torch.randn((B, hk, D, T), generator=g).to(torch.bfloat16)
+    vc = torch.randn((B, hk, D, T), generator=g).to(torch.bfloat16)
+    k, v = kc.transpose(2, 3), vc.transpose(2, 3)          # stride 1 along T
+    rel = (torch.randn((B, T, hq, E), generator=g) * 0.5).to(
+        torch.bfloat16).transpose(1, 2)                    # [B,H,T,E]
+    positions = torch.arange(T)
+    ref = attn_ref.prefill_reference_semantics(q, k, v, rel, positions,
+                                               window)
+    out = tm.attn_prefill_fused(q.to(dev), k.to(dev), v.to(dev), rel.to(dev),
+                                positions.to(dev), positions.to(dev), window)
+    torch.cuda.synchronize()
+    assert out.shape == (B, T, hq, D)
+    assert_out_close(out, ref, f"prefill_fused w={window} {hq}/{hk}")

@@ -59,6 +59,7 @@ SIGNATURES = {
         _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64,
         _c_i64, _c_ptr, _c_ptr, _c_i32, _c_i32, _c_ptr, _c_ptr, _c_ptr,
         _c_i64, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_f32,
+        _c_ptr, _c_i64, _c_i64, _c_i32,
         _c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr]),
 }
 

@@ -112,7 +112,7 @@ def decode_workspace(B, HQ, HKV, device, num_workgroups=0):
 
 def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
                  table_wrap=0, rel=None, min_pages=8, num_workgroups=0,
-                 out=None, lse=None, workspace=None):
+                 out=None, lse=None, workspace=None, return_lse=True):
     """Split-KV paged decode attention (one launch, persistent grid).
 
     q [B, HQ, D] bf16 contiguous (query at position ctx_lens[b]-1);
@@ -144,7 +144,7 @@ def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
     dev = q.device
     if out is None:
         out = torch.empty_like(q)
-    if lse is None:
+    if lse is None and return_lse:
         lse = torch.empty((B, HQ), dtype=torch.float32, device=dev)
     if workspace is None:
         workspace = decode_workspace(B, HQ, HKV, dev, num_workgroups)
@@ -165,7 +165,8 @@ def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
 
 def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, max_seqlen=None,
                    prior_lens=None, k_pool=None, v_pool=None,
-                   block_table=None, out=None, lse=None):
+                   block_table=None, rel=None, out=None, lse=None,
+                   return_lse=True):
     """Varlen causal (optionally windowed) prefill attention on bf16 MFMA.
 
     q [total, HQ, D], k/v [total, HKV, D] bf16 (D contiguous, any token /
@@ -173,7 +174,10 @@ def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, max_seqlen=None,
     [S, bt_stride]) every key, prior context included, is read from
     k_pool/v_pool [num_pages, 16, HKV, D] and prior_lens [S] int32 gives the
     position of each run's first query; the run's own keys must already be
-    in the pool. Returns (out [total, HQ, D] bf16, lse [HQ, total] fp32).
+    in the pool. rel: optional fused relative bias [total, HQ, E] (last
+    axis contiguous, any token/head strides): pair (q, k) of head h adds
+    rel[q_row, h, pos_q - pos_k] inside 0 <= dist < E (attn_prefill.py:
+    115-120). Returns (out [total, HQ, D] bf16, lse [HQ, total] fp32 or None).
     Reference: engine/pyengine/kernels/attn_prefill.py:71-194."""
     total, HQ, D = q.shape
     _check_rows(q, "q")
@@ -203,10 +207,13 @@ def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, max_seqlen=None,
         ks = (k.stride(0), k.stride(1))
         vs = (v.stride(0), v.stride(1))
     assert HQ % HKV == 0
+    if rel is not None:
+        assert rel.dtype == torch.bfloat16 and rel.stride(2) == 1
+        assert rel.shape[:2] == (total, HQ), (rel.shape, total, HQ)
     dev = q.device
     if out is None:
         out = torch.empty((total, HQ, D), dtype=torch.bfloat16, device=dev)
-    if lse is None:
+    if lse is None and return_lse:
         lse = torch.empty((HQ, total), dtype=torch.float32, device=dev)
     _lib.call("tmopt_attn_prefill_varlen", _ptr(q), q.stride(0), q.stride(1),
               None if paged else _ptr(k), ks[0], ks[1],
@@ -215,6 +222,9 @@ def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, max_seqlen=None,
               _ptr(k_pool) if paged else None,
               _ptr(v_pool) if paged else None, _ptr(block_table),
               block_table.stride(0) if paged else 0, page_size, P, HQ, HKV,
-              D, int(window), float(scale), _ptr(out), out.stride(0),
+              D, int(window), float(scale), _ptr(rel),
+              0 if rel is None else rel.stride(0),
+              0 if rel is None else rel.stride(1),
+              0 if rel is None else rel.shape[2], _ptr(out), out.stride(0),
               out.stride(1), _ptr(lse), _stream(dev))
     return out, lse

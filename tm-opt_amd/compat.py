@@ -1,0 +1,121 @@
+"""The reference engine's attention call signatures over the native kernels.
+
+attn_swa / attn_global / attn_prefill_fused take exactly the arguments of
+engine/pyengine/kernels/attn_swa.py:120, attn_global.py:15 and
+attn_prefill.py:144, keep their contract asserts, their model semantics
+(scale 1/head_dim because q/k are RMS-normed, the fused relative bias
+gathered at the clamped backward distance and zeroed out of band) and their
+output layouts, and run the gfx950 kernels of this package:
+
+  * the SWA ring pool [S, W, HK, D] is viewed as W/16 pages per slot and
+    walked as a ring block table (table_wrap = W/16): position p lives in
+    ring slot p % W, exactly RingKV's rule (kv.py:75-76, :99-100);
+  * the global path's per-token flat rows `flat` [B, Lg] (model.py:938-945)
+    are turned back into a block table: rows of one page are consecutive,
+    so page i of row b is flat[b, 16 i] // 16;
+  * the padded [B, H, T, D] prefill batch becomes B packed runs of T tokens
+    (cu_seqlens = 0, T, 2T, ...), read in place when the strides allow and
+    copied to the packed layout otherwise (e.g. channel-major K/V).
+
+No host synchronisation: every helper tensor is built with device ops, so
+the adapters can run inside hipGraph capture.
+"""
+import os
+
+import torch
+
+from . import attn
+
+PAGE = attn.PAGE_SIZE
+
+
+def attn_swa(q, pool_k, pool_v, slots, pos, rel):
+    """SWA decode attention over a ring pool, in place (attn_swa.py:120).
+    q [B, HQ, D] bf16, pool_k/pool_v [S, W, HK, D] bf16, slots/pos [B] i64,
+    rel [B, HQ, W] bf16. Returns [B, HQ, D]."""
+    B, HQ, D = q.shape
+    S, W, HK, _ = pool_k.shape
+    assert q.is_contiguous() and rel.is_contiguous()
+    assert pool_k.is_contiguous() and pool_v.is_contiguous()
+    assert rel.shape == (B, HQ, W), (rel.shape, (B, HQ, W))
+    assert slots.dtype == torch.int64 and pos.dtype == torch.int64
+    assert W % PAGE == 0, "ring length must be a whole number of pages"
+    per = W // PAGE
+    kp = pool_k.view(S * per, PAGE, HK, D)
+    vp = pool_v.view(S * per, PAGE, HK, D)
+    ring = torch.arange(per, device=q.device, dtype=torch.int64)
+    table = (slots[:, None] * per + ring[None, :]).to(torch.int32)
+    ctx = (pos + 1).to(torch.int32)
+    out, _ = attn.decode_paged(q, kp, vp, table, ctx, 1.0 / D, window=W,
+                               table_wrap=per, rel=rel, return_lse=False)
+    return out
+
+
+def attn_global(q, pool_kp, pool_vp, flat, pos, rel, Lg):
+    """Global decode attention over a page pool, in place (attn_global.py:15).
+    q [B, HQ, D] bf16, pool_kp/pool_vp [(P+1), 16, HK, D] bf16, flat [B, Lg]
+    i64 per-token rows (dead columns 0), pos [B] i64, rel [B, HQ, E] bf16.
+    Returns [B, HQ, D]."""
+    B, HQ, D = q.shape
+    assert q.is_contiguous() and rel.is_contiguous()
+    assert pool_kp.is_contiguous() and pool_vp.is_contiguous()
+    assert flat.is_contiguous() and flat.shape == (B, Lg)
+    assert flat.dtype == torch.int64 and pos.dtype == torch.int64
+    ps = pool_kp.shape[1]
+    assert ps == PAGE
+    table = (flat[:, ::ps] // ps).to(torch.int32).contiguous()
+    ctx = (pos + 1).to(torch.int32)
+    out, _ = attn.decode_paged(q, pool_kp, pool_vp, table, ctx, 1.0 / D,
+                               window=0, rel=rel, return_lse=False)
+    return out
+
+
+def _packed(x, B, T, H, D):
+    """[B, H, T, D] view -> [B*T, H, D] with D contiguous and token stride
+    uniform across the batch boundary (a view when possible)."""
+    xt = x.transpose(1, 2)                       # [B, T, H, D]
+    if not (xt.stride(3) == 1 and (B == 1 or xt.stride(0) == T * xt.stride(1))
+            and xt.stride(1) % 8 == 0 and xt.stride(2) % 8 == 0):
+        xt = xt.contiguous()
+    return xt.as_strided((B * T, H, D), (xt.stride(1), xt.stride(2), 1))
+
+
+def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
+                       block_m=64, block_n=64):
+    """Fused prefill attention over in-batch K/V (attn_prefill.py:144).
+    q [B, H, T, D], k/v [B, HK, T, D] bf16 (any strides), rel [B, H, T, E]
+    bf16 with rel.stride(3) == 1, q_positions/kv_positions [T] i64 (the
+    engine's arange), window None (global) or W (SWA, E == W).
+    Returns [B, T, H, D] bf16. block_m / block_n are accepted for signature
+    compatibility; the kernel's tiles are fixed for gfx950."""
+    B, H, T, D = q.shape
+    HK = k.shape[1]
+    E = rel.shape[3]
+    assert k.shape == (B, HK, T, D) and v.shape == (B, HK, T, D)
+    assert rel.shape == (B, H, T, E) and rel.stride(3) == 1
+    assert q_positions.shape == (T,) and kv_positions.shape == (T,)
+    assert q_positions.dtype == torch.int64
+    assert kv_positions.dtype == torch.int64
+    assert H % HK == 0
+    if window is not None:
+        assert E == window, (E, window)
+    if q_positions.device.type == "cpu" or os.environ.get("TMOPT_CHECK"):
+        # positions are derived in-kernel from indices: both must be arange
+        ar = torch.arange(T, device=q_positions.device)
+        assert torch.equal(q_positions, ar) and torch.equal(
+            kv_positions.to(ar.device), ar), "positions must be arange(T)"
+    dev = q.device
+    qp = _packed(q, B, T, H, D)
+    kp = _packed(k, B, T, HK, D)
+    vp = _packed(v, B, T, HK, D)
+    rt = rel.transpose(1, 2)                     # [B, T, H, E]
+    if not (B == 1 or rt.stride(0) == T * rt.stride(1)):
+        rt = rt.contiguous()
+    relp = rt.as_strided((B * T, H, E), (rt.stride(1), rt.stride(2), 1))
+    out = torch.empty((B, T, H, D), dtype=q.dtype, device=dev)
+    cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=dev)
+    attn.prefill_varlen(qp, kp, vp, cu, 1.0 / D,
+                        window=0 if window is None else int(window),
+                        max_seqlen=T, rel=relp, out=out.view(B * T, H, D),
+                        return_lse=False)
+    return out

@@ -577,8 +577,9 @@ extern "C" int tmopt_attn_decode_paged(
     void* workspace, size_t workspace_bytes, tmopt_stream_t stream) {
   clear_error();
   if (B == 0) return TMOPT_OK;
-  TMOPT_REQUIRE(B > 0 && B <= kMaxB, TMOPT_EUNSUPPORTED,
-                "decode: B=%d outside [0, %d]", B, kMaxB);
+  TMOPT_REQUIRE(B > 0, TMOPT_EINVAL, "decode: B=%d", B);
+  TMOPT_REQUIRE(B <= kMaxB, TMOPT_EUNSUPPORTED, "decode: B=%d above %d", B,
+                kMaxB);
   TMOPT_REQUIRE(q && k_pool && v_pool && block_table && ctx_lens && out,
                 TMOPT_EINVAL, "decode: null tensor pointer");
   TMOPT_REQUIRE(D == kD, TMOPT_EUNSUPPORTED, "decode: D=%d (only 128)", D);

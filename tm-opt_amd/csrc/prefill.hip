@@ -71,6 +71,9 @@ struct PrefillArgs {
   int64_t o_st, o_sh;
   float* lse;        // [HQ, cu[S]]
   int S;
+  const __bf16* rel; // optional fused relative bias, rows like q
+  int64_t r_st, r_sh;
+  int rel_extent;
 };
 
 // LDS column of key kappa (0..63) in a V^T row: within each 16-key chunk the
@@ -86,7 +89,7 @@ __device__ __forceinline__ int vt_off(int d, int ch, int b) {
   return d * kVRow + ((ch ^ ((d >> 3) & 7)) << 4) + b;
 }
 
-template <int REP>
+template <int REP, bool REL>
 __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   constexpr int BQ = 256 / REP;   // queries per work-group
   constexpr int QSUB = BQ / 32;   // 32-query sub-blocks per head
@@ -279,8 +282,27 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     }
 
     // ---- online softmax -------------------------------------------------
-    // The max runs on the raw scores (scale > 0 commutes with max); each
-    // probability is then one fma + exp2: p = 2^(s * scale*log2e - m).
+    // Without a bias the max runs on the raw scores (scale > 0 commutes with
+    // max) and each probability is one fma + exp2: p = 2^(s*scale*log2e - m).
+    // With the fused relative bias (attn_prefill.py:115-120) the scores are
+    // first moved to the log2 domain, s*scale*log2e + rel*log2e, gathered at
+    // rel[q, h, dist] for 0 <= dist < E and zero outside the band.
+    float sl2 = a.scale_log2;
+    if constexpr (REL) {
+      const __bf16* rrow = a.rel + (int64_t)(t0 + (qok ? qi : 0)) * a.r_st +
+                           (int64_t)head * a.r_sh;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const int kp = kt + 32 * kb + 8 * (j >> 2) + 4 * h2 + (j & 3);
+          const int dist = qpos - kp;
+          const bool band = qok && dist >= 0 && dist < a.rel_extent;
+          const float bias = band ? (float)rrow[dist] : 0.0f;
+          sc[kb][j] = __builtin_fmaf(sc[kb][j], a.scale_log2, bias * kLog2e);
+        }
+      sl2 = 1.0f;
+    }
     if (!full) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
@@ -304,7 +326,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     // tile's max exceeds it by more than kLazy, so probabilities stay below
     // 2^kLazy and O^T / l are rescaled on few tiles; O / l and the LSE are
     // exact for any reference point.
-    const float m_cand = mx * a.scale_log2;
+    const float m_cand = mx * sl2;
     const bool move = m_cand > m_run + kLazy;
     const float m_new = move ? m_cand : m_run;
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
@@ -320,9 +342,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float p0 = fast_exp2(
-              __builtin_fmaf(sc[kb][8 * kk + 2 * e], a.scale_log2, -m_use));
+              __builtin_fmaf(sc[kb][8 * kk + 2 * e], sl2, -m_use));
           const float p1 = fast_exp2(
-              __builtin_fmaf(sc[kb][8 * kk + 2 * e + 1], a.scale_log2, -m_use));
+              __builtin_fmaf(sc[kb][8 * kk + 2 * e + 1], sl2, -m_use));
           psum += p0 + p1;
           pw[e] = pack_bf16x2_rn(p0, p1);
         }
@@ -382,7 +404,12 @@ void launch(const PrefillArgs& a, int S, int max_seqlen, hipStream_t st) {
   constexpr int BQ = 256 / REP;
   const int nqb = (max_seqlen + BQ - 1) / BQ;
   dim3 grid(a.HKV, S, nqb);
-  hipLaunchKernelGGL(prefill_kernel<REP>, grid, dim3(512), 2 * kStage, st, a);
+  if (a.rel)
+    hipLaunchKernelGGL((prefill_kernel<REP, true>), grid, dim3(512),
+                       2 * kStage, st, a);
+  else
+    hipLaunchKernelGGL((prefill_kernel<REP, false>), grid, dim3(512),
+                       2 * kStage, st, a);
 }
 
 }  // namespace
@@ -397,7 +424,8 @@ extern "C" int tmopt_attn_prefill_varlen(
     const int32_t* prior_lens, int num_seqs, int max_seqlen_q,
     const void* k_pool, const void* v_pool, const int32_t* block_table,
     int64_t bt_stride, int page_size, int64_t num_pages, int HQ, int HKV, int D,
-    int window, float scale, void* out, int64_t o_stride_tok,
+    int window, float scale, const void* rel, int64_t rel_stride_tok,
+    int64_t rel_stride_head, int rel_extent, void* out, int64_t o_stride_tok,
     int64_t o_stride_head, float* lse, tmopt_stream_t stream) {
   clear_error();
   if (num_seqs == 0 || max_seqlen_q == 0) return TMOPT_OK;
@@ -414,6 +442,8 @@ extern "C" int tmopt_attn_prefill_varlen(
                 "prefill: HQ/HKV=%d not in {4, 8}", rep);
   TMOPT_REQUIRE(window >= 0, TMOPT_EINVAL, "prefill: window=%d", window);
   TMOPT_REQUIRE(scale > 0.0f, TMOPT_EINVAL, "prefill: scale must be > 0");
+  TMOPT_REQUIRE(rel == nullptr || rel_extent > 0, TMOPT_EINVAL,
+                "prefill: rel_extent=%d", rel_extent);
   const bool paged = block_table != nullptr;
   if (paged) {
     TMOPT_REQUIRE(k_pool && v_pool && page_size > 0 && bt_stride > 0 &&
@@ -468,6 +498,10 @@ extern "C" int tmopt_attn_prefill_varlen(
   a.o_sh = o_stride_head;
   a.lse = lse;
   a.S = num_seqs;
+  a.rel = (const __bf16*)rel;
+  a.r_st = rel_stride_tok;
+  a.r_sh = rel_stride_head;
+  a.rel_extent = rel ? rel_extent : 0;
   hipStream_t st = (hipStream_t)stream;
   if (rep == 8)
     launch<8>(a, num_seqs, max_seqlen_q, st);

@@ -1,0 +1,123 @@
+"""hipGraph capture of the decode step's attention work.
+
+The reference captures its whole pooled decode step per device segment with
+CUDA graphs (engine/pyengine/graphrun.py:76-380): static input buffers, the
+batch padded to max_batch with a scratch slot, and one capture per 512-token
+bucket of the padded key length (graphrun.py:339-343) because its gather
+indices are shaped by that length.
+
+Here the attention part of a step is, per layer, one KV-cache append
+(tmopt_kv_write_paged: the new token of every row goes to page
+ctx/16 of its block table) and one paged decode (tmopt_attn_decode_paged).
+Both read positions and lengths from device memory and launch grids that do
+not depend on them (the decode grid is the persistent one), so ONE capture
+serves every step for the lifetime of the buffers: no buckets, no
+recapture. Nothing inside the captured region allocates, synchronises, or
+issues a memset (workspaces are allocated before capture).
+
+StepGraph captures any callable that works on static buffers (warm-up
+twice on a side stream, then capture, as graphrun.py:260-301 does);
+DecodeStepGraph builds the multi-layer decode-attention step on top of it.
+"""
+import torch
+
+from . import attn
+
+
+class StepGraph:
+    """Capture `fn` (a callable touching only static device buffers)."""
+
+    def __init__(self, fn, device=None):
+        self.fn = fn
+        self.device = torch.device(device or "cuda")
+        self.graph = None
+        self.pool = None
+        self.stream = None
+
+    def capture(self, warmup=2):
+        with torch.cuda.device(self.device):
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                for _ in range(warmup):
+                    self.fn()
+            torch.cuda.current_stream().wait_stream(s)
+            torch.cuda.synchronize()
+            self.pool = torch.cuda.graph_pool_handle()
+            self.stream = torch.cuda.Stream()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=self.pool, stream=self.stream):
+                self.fn()
+            self.graph = g
+        return self
+
+    def replay(self):
+        assert self.graph is not None, "capture() first"
+        self.graph.replay()
+
+
+class DecodeStepGraph:
+    """Decode-step attention for a stack of layers, captured once.
+
+    layers: list of dicts with k_pool, v_pool ([P, 16, HKV, D] bf16),
+    block_table ([MB, width] int32, static), window (0 = global) and
+    table_wrap (ring tables for sliding-window pools, 0 otherwise).
+    Static inputs the host fills before each replay (outside the graph):
+      q      [L, MB, HQ, D]  bf16   query of every row, per layer
+      k_new  [L, MB, HKV, D] bf16   the step's new key / value rows
+      v_new  [L, MB, HKV, D] bf16
+      ctx    [MB] int32             keys after this step's append (pos + 1)
+    Outputs after replay: out [L, MB, HQ, D] bf16, lse [L, MB, HQ] fp32.
+    Rows without a live sequence should point at a scratch slot / page with
+    ctx = 1, as the reference's dead rows do (kv.py:223-228)."""
+
+    def __init__(self, layers, max_batch, HQ, HKV, D=attn.HEAD_DIM,
+                 scale=None, device="cuda", min_pages=8, num_workgroups=0):
+        self.layers = layers
+        self.L = len(layers)
+        self.MB, self.HQ, self.HKV, self.D = max_batch, HQ, HKV, D
+        self.scale = scale if scale is not None else D ** -0.5
+        dev = torch.device(device)
+        bf = torch.bfloat16
+        self.q = torch.zeros((self.L, max_batch, HQ, D), dtype=bf, device=dev)
+        self.k_new = torch.zeros((self.L, max_batch, HKV, D), dtype=bf,
+                                 device=dev)
+        self.v_new = torch.zeros_like(self.k_new)
+        self.ctx = torch.ones(max_batch, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(max_batch, dtype=torch.int32, device=dev)
+        self.out = torch.zeros((self.L, max_batch, HQ, D), dtype=bf,
+                               device=dev)
+        self.lse = torch.zeros((self.L, max_batch, HQ), dtype=torch.float32,
+                               device=dev)
+        # one workspace serves every layer: the layers run in stream order
+        self.workspace = attn.decode_workspace(max_batch, HQ, HKV, dev,
+                                               num_workgroups)
+        self.min_pages = min_pages
+        self.num_workgroups = num_workgroups
+        self.graph = StepGraph(self._step, dev)
+
+    def _step(self):
+        torch.sub(self.ctx, 1, out=self.pos)
+        for l, ly in enumerate(self.layers):
+            attn.kv_write_paged(self.k_new[l], self.v_new[l],
+                                ly["block_table"], self.pos, ly["k_pool"],
+                                ly["v_pool"],
+                                table_wrap=ly.get("table_wrap", 0))
+            attn.decode_paged(self.q[l], ly["k_pool"], ly["v_pool"],
+                              ly["block_table"], self.ctx, self.scale,
+                              window=ly.get("window", 0),
+                              table_wrap=ly.get("table_wrap", 0),
+                              min_pages=self.min_pages,
+                              num_workgroups=self.num_workgroups,
+                              out=self.out[l], lse=self.lse[l],
+                              workspace=self.workspace)
+
+    def run_eager(self):
+        self._step()
+
+    def capture(self):
+        self.graph.capture()
+        return self
+
+    def replay(self):
+        self.graph.replay()

@@ -125,6 +125,68 @@ def bench_prefill(tm, wl, window, steps, warmup, n_sets=2):
     }
 
 
+def _event_ms(fn, reps):
+    fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def bench_mixed(tm, wl, steps, warmup):
+    """Config 5: the 66-layer mixed step captured as one hipGraph; per-step
+    time from the replays, per-layer parts timed eagerly with events."""
+    graph = importlib.import_module("tm-opt_amd.graph")
+    st = wl.config5(device="cuda")
+    ms = graph.MixedStepGraph(st).capture()
+    for _ in range(warmup):
+        ms.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        ms.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    step_ms = e0.elapsed_time(e1) / steps
+    kinds = {}
+    for name, l in (("global", 3), ("swa", 0)):
+        parts = {p: _event_ms(lambda p=p: ms.layer(l, (p,)), 3)
+                 for p in ("kv", "prefill", "decode")}
+        dec_b = st.decode_bytes(l)
+        pf = st.prefill_flops(l)
+        kinds[name] = {
+            "us_kv_write": parts["kv"] * 1e3,
+            "us_prefill": parts["prefill"] * 1e3,
+            "us_decode": parts["decode"] * 1e3,
+            "decode_gbs": dec_b / (parts["decode"] * 1e-3) / 1e9,
+            "prefill_tflops": pf / (parts["prefill"] * 1e-3) / 1e12,
+            "kv_write_gbs": st.kv_write_bytes() / (parts["kv"] * 1e-3) / 1e9,
+            "decode_bytes": dec_b, "prefill_flops": pf}
+    n_g = sum(st.is_global)
+    n_s = st.n_layers - n_g
+    dec_total = sum(st.decode_bytes(l) for l in range(st.n_layers))
+    pf_total = sum(st.prefill_flops(l) for l in range(st.n_layers))
+    bound_ms = (dec_total / (HBM_PEAK_GBS * 1e9) +
+                pf_total / (BF16_PEAK_TFLOPS * 1e12)) * 1e3
+    return {"workload": "C5 mixed step, 66 layers (16 global + 50 SWA 4096)",
+            "ms_per_step_graph": step_ms,
+            "us_per_layer_mean": step_ms * 1e3 / st.n_layers,
+            "layers": {"global": n_g, "swa": n_s},
+            "per_layer_kind": kinds,
+            "decode_bytes_per_step": dec_total,
+            "prefill_flops_per_step": pf_total,
+            "roofline_lower_bound_ms": bound_ms,
+            "frac_of_bound": bound_ms / step_ms,
+            "seed": st.meta["seed"]}
+
+
 def cpu_baseline_decode(wl, sample_b=8):
     """fp32 torch oracle on the host cores over the first sample_b
     sequences of config 2; GB/s of algorithmic bytes."""
@@ -192,6 +254,13 @@ def main():
                   f" us {r['tflops_events']:.0f} TFLOP/s", file=sys.stderr,
                   flush=True)
             extra["C4_prefill_" + ("global" if win == 0 else f"swa{win}")] = r
+    if args.only in ("", "c5"):
+        r = bench_mixed(tm, wl, max(3, args.steps // 10), 2)
+        print(f"[bench] C5 step {r['ms_per_step_graph']:.2f} ms "
+              f"({r['frac_of_bound'] * 100:.0f}% of the roofline bound "
+              f"{r['roofline_lower_bound_ms']:.2f} ms)", file=sys.stderr,
+              flush=True)
+        extra["C5_mixed_step"] = r
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline_decode(wl)

@@ -121,3 +121,58 @@ class DecodeStepGraph:
 
     def replay(self):
         self.graph.replay()
+
+
+class MixedStepGraph:
+    """Config-5 step: for every layer, append the step's tokens (chunked
+    prefill runs + one token per decode row) through the layer's block
+    table, run the paged chunked prefill, then the paged decode. All three
+    kernels per layer are captured into ONE hipGraph for the whole step."""
+
+    def __init__(self, step, min_pages=8, num_workgroups=0):
+        self.s = step
+        dev = step.q_decode.device
+        B, HQ, D = step.q_decode.shape
+        HKV = step.pool_g[0].shape[2]
+        self.n_chunks = len(step.chunk_lens)
+        self.max_chunk = max(step.chunk_lens)
+        self.out_p = torch.empty_like(step.q_prefill)
+        self.out_d = torch.empty_like(step.q_decode)
+        self.lse_d = torch.empty((B, HQ), dtype=torch.float32, device=dev)
+        self.ws = attn.decode_workspace(B, HQ, HKV, dev, num_workgroups)
+        self.min_pages, self.num_workgroups = min_pages, num_workgroups
+        self.graph = StepGraph(self.run_eager, dev)
+
+    def layer(self, l, parts=("kv", "prefill", "decode")):
+        s = self.s
+        kp, vp = s.pool_g if s.is_global[l] else s.pool_s
+        w = 0 if s.is_global[l] else s.window
+        t = s.tables[l]
+        if "kv" in parts:
+            attn.kv_write_paged(s.k_new, s.v_new, t, s.start_all, kp, vp,
+                                cu_seqlens=s.cu_all,
+                                max_seqlen=self.max_chunk)
+        if "prefill" in parts:
+            attn.prefill_varlen(s.q_prefill, None, None, s.cu_chunks,
+                                s.scale, window=w, max_seqlen=self.max_chunk,
+                                prior_lens=s.prior, k_pool=kp, v_pool=vp,
+                                block_table=t[:self.n_chunks],
+                                out=self.out_p, return_lse=False)
+        if "decode" in parts:
+            attn.decode_paged(s.q_decode, kp, vp, t[self.n_chunks:],
+                              s.dec_ctx, s.scale, window=w,
+                              min_pages=self.min_pages,
+                              num_workgroups=self.num_workgroups,
+                              out=self.out_d, lse=self.lse_d,
+                              workspace=self.ws)
+
+    def run_eager(self):
+        for l in range(self.s.n_layers):
+            self.layer(l)
+
+    def capture(self):
+        self.graph.capture()
+        return self
+
+    def replay(self):
+        self.graph.replay()

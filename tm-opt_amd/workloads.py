@@ -227,3 +227,117 @@ def paged_layout(lens, g, pool_factor=2, prior=None):
         table[i, :n] = perm[off:off + n].to(torch.int32)
         off += n
     return table, P
+
+
+# --------------------------------------------------------------------------
+# config 5: mixed continuous-batching step over 66 layers
+# --------------------------------------------------------------------------
+
+@dataclass
+class MixedStep:
+    """One step of config 5 for every layer. Rows 0..n_chunks-1 of each
+    layer's block table are the chunked-prefill runs, the rest the decode
+    rows. Each layer walks its own shuffled table over one physical pool per
+    layer kind (global / sliding window): a layer's footprint (GBs) is far
+    above the 256 MB Infinity Cache, so its HBM traffic equals that of a
+    private pool."""
+    n_layers: int
+    window: int
+    is_global: list             # per layer
+    tables: list                # per layer [R, width] int32
+    pool_g: tuple               # (k, v) [Pg, 16, HKV, D]
+    pool_s: tuple
+    chunk_lens: list
+    chunk_prior: list
+    dec_ctx: torch.Tensor       # [96] int32 (after this step's append)
+    q_prefill: torch.Tensor     # [sum chunks, HQ, D]
+    q_decode: torch.Tensor      # [96, HQ, D]
+    k_new: torch.Tensor         # [sum chunks + 96, HKV, D]
+    v_new: torch.Tensor
+    cu_all: torch.Tensor        # [R + 1] int32 (chunks, then 1 per row)
+    start_all: torch.Tensor     # [R] int32
+    cu_chunks: torch.Tensor     # [n_chunks + 1] int32
+    prior: torch.Tensor         # [n_chunks] int32
+    scale: float = SCALE
+    meta: dict = field(default_factory=dict)
+
+    def decode_bytes(self, layer):
+        n = self.dec_ctx.to(torch.int64).cpu()
+        if not self.is_global[layer]:
+            n = torch.minimum(n, torch.tensor(self.window))
+        B, hq, d = self.q_decode.shape
+        hkv = self.pool_g[0].shape[2]
+        return int(n.sum()) * hkv * d * 4 + B * hq * d * 4 + B * hq * 4 + \
+            int(((n + PAGE - 1) // PAGE).sum()) * 4 + B * 4
+
+    def prefill_flops(self, layer):
+        w = 0 if self.is_global[layer] else self.window
+        hq, d = self.q_prefill.shape[1], self.q_prefill.shape[2]
+        return 4 * d * hq * visible_pairs(self.chunk_lens, w,
+                                          self.chunk_prior)
+
+    def kv_write_bytes(self):
+        T = self.k_new.shape[0]
+        hkv, d = self.k_new.shape[1], self.k_new.shape[2]
+        return 2 * 2 * T * hkv * d * 2 + T * 8
+
+
+def config5(device="cuda", n_layers=66, window=4096, n_decode=96,
+            chunk=2048, prior=4096, n_chunks=2, lo=1024, hi=65536):
+    g = generator(5, "cpu")
+    u = torch.rand(n_decode, generator=g, dtype=torch.float64)
+    ctx = torch.floor(torch.exp(math.log(lo) + u * (math.log(hi) -
+                                                    math.log(lo)))).long()
+    ctx = torch.clamp(ctx, lo, hi)
+    chunk_tot = prior + chunk
+    R = n_chunks + n_decode
+    log_pages = [(chunk_tot + PAGE - 1) // PAGE] * n_chunks + \
+        [int((c + PAGE - 1) // PAGE) for c in ctx]
+    width = max(log_pages)
+    # backed logical pages per row: global = all; window = pages that hold
+    # a key some query of the row can see
+    first_s = [0] * n_chunks + [int(max(0, int(c) - window) // PAGE)
+                                for c in ctx]
+    Pg = sum(log_pages) + 1
+    Ps = sum(lp - f for lp, f in zip(log_pages, first_s)) + 1
+    gd = generator(5, device) if device != "cpu" else g
+    hkv = HKV
+
+    def pool(P):
+        k = _randn_bf16((P, PAGE, hkv, D), gd, device)
+        v = _randn_bf16((P, PAGE, hkv, D), gd, device)
+        return k, v
+
+    pool_g, pool_s = pool(Pg), pool(Ps)
+    is_global = [i % 4 == 3 for i in range(n_layers)]
+    tables = []
+    for i in range(n_layers):
+        P = Pg if is_global[i] else Ps
+        perm = torch.randperm(P - 1, generator=g).to(torch.int32)
+        t = torch.full((R, width), P - 1, dtype=torch.int32)  # poison page
+        off = 0
+        for r in range(R):
+            f = 0 if is_global[i] else first_s[r]
+            n = log_pages[r] - f
+            t[r, f:f + n] = perm[off:off + n]
+            off += n
+        tables.append(t.to(device))
+    T_new = n_chunks * chunk + n_decode
+    cu_all = [0]
+    for r in range(R):
+        cu_all.append(cu_all[-1] + (chunk if r < n_chunks else 1))
+    start_all = [prior] * n_chunks + [int(c) - 1 for c in ctx]
+    ic = lambda x: torch.tensor(x, dtype=torch.int32, device=device)
+    return MixedStep(
+        n_layers=n_layers, window=window, is_global=is_global, tables=tables,
+        pool_g=pool_g, pool_s=pool_s, chunk_lens=[chunk] * n_chunks,
+        chunk_prior=[prior] * n_chunks, dec_ctx=ctx.to(torch.int32).to(device),
+        q_prefill=_randn_bf16((n_chunks * chunk, HQ, D), gd, device),
+        q_decode=_randn_bf16((n_decode, HQ, D), gd, device),
+        k_new=_randn_bf16((T_new, hkv, D), gd, device),
+        v_new=_randn_bf16((T_new, hkv, D), gd, device),
+        cu_all=ic(cu_all), start_all=ic(start_all),
+        cu_chunks=ic([i * chunk for i in range(n_chunks + 1)]),
+        prior=ic([prior] * n_chunks),
+        meta={"seed": SEED0 + 5, "global_pages": Pg, "swa_pages": Ps,
+              "decode_ctx": ctx.tolist()})

@@ -187,9 +187,9 @@ def bench_mixed(tm, wl, steps, warmup):
             "seed": st.meta["seed"]}
 
 
-def cpu_baseline_decode(wl, sample_b=8):
-    """fp32 torch oracle on the host cores over the first sample_b
-    sequences of config 2; GB/s of algorithmic bytes."""
+def cpu_baseline_decode(wl, sample_b=64, reps=5):
+    """fp32 torch oracle on the host cores over (by default all 64)
+    sequences of config 2; GB/s of algorithmic bytes, median of reps."""
     from oracle import attn_ref
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
@@ -199,17 +199,42 @@ def cpu_baseline_decode(wl, sample_b=8):
                         c.block_table[sel], c.ctx_lens[sel], c.window,
                         c.scale, c.meta)
     times = []
-    for _ in range(3):
+    for _ in range(reps):
         t0 = time.perf_counter()
         attn_ref.decode_paged(sub.q, sub.k_pool, sub.v_pool,
                               sub.block_table, sub.ctx_lens, sub.scale)
         times.append(time.perf_counter() - t0)
-    t = sorted(times)[1]
+    t = sorted(times)[len(times) // 2]
     return {"value": sub.algorithmic_bytes() / t / 1e9, "unit": "GB/s",
             "cores": threads, "kind": "port",
-            "sample": f"config 2, first {sample_b} of 64 sequences "
-                      f"({int(sub.ctx_lens.sum())} keys), median of 3",
+            "sample": f"config 2, {sample_b} of 64 sequences "
+                      f"({int(sub.ctx_lens.sum())} keys), fp32 torch oracle, "
+                      f"median of {reps} runs ({sum(times):.1f} s total)",
             "seconds": t}
+
+
+def calibrate_copy():
+    """A plain copy of known size (1 GiB read + 1 GiB written) for the
+    FETCH_SIZE / WRITE_SIZE calibration of the HBM-traffic counters."""
+    x = torch.ones(1 << 29, dtype=torch.bfloat16, device="cuda")
+    y = torch.empty_like(x)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "copy", "bytes_read": x.numel() * 2,
+                      "bytes_written": y.numel() * 2}), flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per decode launch from the committed rocprofv3 PMC summary
+    (profiles/decode_c2_traffic.json), scaled by the copy calibration."""
+    path = os.path.join(ROOT, "profiles", "decode_c2_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        t = json.load(f)
+    return int(t["fetch_bytes_per_launch"] + t["write_bytes_per_launch"])
 
 
 def main():
@@ -221,6 +246,7 @@ def main():
     ap.add_argument("--min-pages", type=int, default=8)
     ap.add_argument("--wgs", type=int, default=0)
     ap.add_argument("--only", default="")
+    ap.add_argument("--calibrate-copy", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the paged-"
@@ -230,6 +256,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     tm = importlib.import_module("tm-opt_amd")
     wl = importlib.import_module("tm-opt_amd.workloads")
     tm._lib.load()
@@ -284,7 +313,7 @@ def main():
                      "achieved": round(head["gbs_events"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["gbs_events"] / HBM_PEAK_GBS, 4),
-                     "traffic": None,
+                     "traffic": measured_traffic(),
                      "kernel": "decode_kernel<8,false> + decode_combine_kernel",
                      "bytes_per_launch": head["bytes_per_launch"],
                      "us_per_launch": round(head["us_per_launch_events"], 2)},

@@ -46,6 +46,31 @@ def test_ragged_lengths(tm, dev, window, hq, hkv):
     assert_lse_close(lse, ref_l, f"ragged w={window} {hq}/{hkv}")
 
 
+@pytest.mark.parametrize("hq,hkv", [(8, 1), (16, 2), (24, 3), (32, 4),
+                                    (64, 16)])
+def test_every_row_written(tm, dev, hq, hkv):
+    """The work-group -> (KV head, run, query block) schedule covers every
+    row: 70 runs (more than one wave's worth of runs) of ragged lengths,
+    outputs and LSE pre-filled with NaN, every head count branch of the
+    XCD mapping (8 % HKV == 0, HKV % 8 == 0, neither)."""
+    g = torch.Generator().manual_seed(31)
+    lens = torch.randint(1, 90, (70,), generator=g).tolist()
+    lens[5] = 300                     # one long run: many empty levels
+    case = _wl().make_prefill("sched", 24, lens=lens, window=0, hq=hq,
+                              hkv=hkv)
+    ref_o, ref_l = attn_ref.prefill_varlen(case.q, case.k, case.v,
+                                           case.cu_seqlens, case.scale)
+    T = case.q.shape[0]
+    out = torch.full((T, hq, 128), float("nan"), dtype=torch.bfloat16,
+                     device=dev)
+    lse = torch.full((hq, T), float("nan"), dtype=torch.float32, device=dev)
+    tm.prefill_varlen(case.q.to(dev), case.k.to(dev), case.v.to(dev),
+                      case.cu_seqlens.to(dev), case.scale, out=out, lse=lse)
+    torch.cuda.synchronize()
+    assert_out_close(out.cpu(), ref_o, f"schedule {hq}/{hkv}")
+    assert_lse_close(lse.cpu(), ref_l, f"schedule {hq}/{hkv}")
+
+
 def test_strided_inputs(tm, dev):
     """K/V as head slices of a wider tensor and Q with padded rows; the
     output written into a strided view."""

@@ -32,9 +32,15 @@
 //  * Tiles wholly outside the causal/window band are never visited; only
 //    tiles that straddle the diagonal, the window start or the run end pay
 //    for per-element masking.
-//  * Grid (HKV, runs, query blocks) with the query-block index reversed, so
-//    the hardware dispatches the heaviest blocks (most keys) first, level by
-//    level, and the light ones fill the tail.
+//  * A 1-D grid walks the (KV head, run, query block) items in "levels":
+//    level z holds query block nqb_max-1-z of every run that has one, so the
+//    heaviest blocks (most keys) are dispatched first and the light ones
+//    fill the tail. Empty (run, block) pairs are compacted away and the
+//    items are dealt to the 8 XCDs in turn (the dispatcher sends work-group
+//    i to XCD i % 8), with each KV head kept on its own XCDs: every XCD gets
+//    an equal share of every level and only one KV head's keys pass through
+//    its L2. A plain (head, run, block) grid maps runs to XCDs by index and
+//    left half of the XCDs idle for half the launch on mixed lengths.
 #include "common.h"
 
 namespace tmopt {
@@ -71,6 +77,7 @@ struct PrefillArgs {
   int64_t o_st, o_sh;
   float* lse;        // [HQ, cu[S]]
   int S;
+  int nqb_max;       // query blocks of the longest run
   const __bf16* rel; // optional fused relative bias, rows like q
   int64_t r_st, r_sh;
   int rel_extent;
@@ -89,6 +96,85 @@ __device__ __forceinline__ int vt_off(int d, int ch, int b) {
   return d * kVRow + ((ch ^ ((d >> 3) & 7)) << 4) + b;
 }
 
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// query blocks of run s (lane-varying s)
+__device__ __forceinline__ int run_blocks(const PrefillArgs& a, int s,
+                                          int BQ) {
+  const int len = a.cu[s + 1] - a.cu[s];
+  return (len + BQ - 1) / BQ;
+}
+
+// items of one KV head in levels [0, z): a run with nb blocks has one item
+// on each level z' >= nqb_max - nb. nb0: blocks of run `lane` (0 past S).
+__device__ __forceinline__ int items_before(const PrefillArgs& a, int z,
+                                            int BQ, int lane, int nb0) {
+  int c = max(0, nb0 - a.nqb_max + z);
+  for (int s = lane + 64; s < a.S; s += 64)
+    c += max(0, run_blocks(a, s, BQ) - a.nqb_max + z);
+  return __builtin_amdgcn_readfirstlane(wave_sum(c));
+}
+
+struct Work {
+  int kvh, seq, qb;  // seq < 0: nothing to do
+};
+
+// Work item of this work-group (computed by every wave, identically).
+// Work-group L runs on XCD L % 8 as the L/8-th one there. KV heads are
+// spread over the XCDs (8 % HKV == 0: 8/HKV XCDs per head; HKV % 8 == 0:
+// HKV/8 heads per XCD; otherwise round robin), and each head's items, in
+// level order, are dealt to its XCDs in turn.
+__device__ __forceinline__ Work schedule(const PrefillArgs& a, int BQ,
+                                         int lane) {
+  const int L = blockIdx.x;
+  int kvh, i;
+  if (a.HKV <= 8 && 8 % a.HKV == 0) {
+    const int R = 8 / a.HKV;
+    kvh = (L & 7) / R;
+    i = (L >> 3) * R + (L & 7) % R;
+  } else if (a.HKV % 8 == 0) {
+    const int R = a.HKV / 8;
+    kvh = (L & 7) + 8 * ((L >> 3) % R);
+    i = (L >> 3) / R;
+  } else {
+    kvh = L % a.HKV;
+    i = L / a.HKV;
+  }
+  Work w{kvh, -1, 0};
+  const int nb0 = lane < a.S ? run_blocks(a, lane, BQ) : 0;
+  const int total = items_before(a, a.nqb_max, BQ, lane, nb0);
+  if (i >= total) return w;
+  // level z: the last one with items_before(z) <= i
+  int lo = 0, hi = a.nqb_max;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (items_before(a, mid, BQ, lane, nb0) <= i) lo = mid; else hi = mid;
+  }
+  int rem = i - items_before(a, lo, BQ, lane, nb0);
+  const int need = a.nqb_max - lo;  // runs with at least this many blocks
+  for (int s0 = 0; s0 < a.S; s0 += 64) {
+    const int s = s0 + lane;
+    const bool act =
+        s < a.S && (s0 == 0 ? nb0 : run_blocks(a, s, BQ)) >= need;
+    const uint64_t m = __builtin_amdgcn_ballot_w64(act);
+    const int pop = __builtin_popcountll(m);
+    if (rem < pop) {
+      const int rank = __builtin_amdgcn_mbcnt_hi(
+          (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(act && rank == rem);
+      w.seq = s0 + __builtin_ctzll(hit);
+      w.qb = a.nqb_max - 1 - lo;
+      return w;
+    }
+    rem -= pop;
+  }
+  return w;  // not reached for i < total
+}
+
 template <int REP, bool REL>
 __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   constexpr int BQ = 256 / REP;   // queries per work-group
@@ -99,14 +185,15 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   const int w = tid >> 6;         // 8 waves: one 32-row block each
   const int l32 = lane & 31;
   const int h2 = lane >> 5;       // lane half
-  const int kvh = blockIdx.x;
-  const int seq = blockIdx.y;
-  const int qb = gridDim.z - 1 - blockIdx.z;
+  const Work wk = schedule(a, BQ, lane);
+  if (wk.seq < 0) return;
+  const int kvh = wk.kvh;
+  const int seq = wk.seq;
+  const int qb = wk.qb;
 
   const int t0 = as_const(a.cu)[seq];
   const int len = as_const(a.cu)[seq + 1] - t0;
   const int q0 = qb * BQ;
-  if (q0 >= len) return;
   const int prior = a.prior ? as_const(a.prior)[seq] : 0;
   const int nk = prior + len;                 // keys of this run
   const int qn = min(BQ, len - q0);
@@ -400,10 +487,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 }
 
 template <int REP>
-void launch(const PrefillArgs& a, int S, int max_seqlen, hipStream_t st) {
+void launch(PrefillArgs a, int S, int max_seqlen, hipStream_t st) {
   constexpr int BQ = 256 / REP;
-  const int nqb = (max_seqlen + BQ - 1) / BQ;
-  dim3 grid(a.HKV, S, nqb);
+  a.nqb_max = (max_seqlen + BQ - 1) / BQ;
+  // HKV * items-per-head work-groups, rounded up to whole XCD rounds
+  const int64_t items = (int64_t)S * a.nqb_max;
+  int64_t n = a.HKV * items;
+  if (a.HKV <= 8 && 8 % a.HKV == 0) n = 8 * ((items + 8 / a.HKV - 1) / (8 / a.HKV));
+  dim3 grid((unsigned)n);
   if (a.rel)
     hipLaunchKernelGGL((prefill_kernel<REP, true>), grid, dim3(512),
                        2 * kStage, st, a);
@@ -444,6 +535,14 @@ extern "C" int tmopt_attn_prefill_varlen(
   TMOPT_REQUIRE(scale > 0.0f, TMOPT_EINVAL, "prefill: scale must be > 0");
   TMOPT_REQUIRE(rel == nullptr || rel_extent > 0, TMOPT_EINVAL,
                 "prefill: rel_extent=%d", rel_extent);
+  {
+    const int bq = 256 / rep;
+    const int64_t blocks =
+        (int64_t)HKV * num_seqs * ((max_seqlen_q + bq - 1) / bq) + 8 * 8;
+    TMOPT_REQUIRE(blocks < 0x7fffffffll, TMOPT_EUNSUPPORTED,
+                  "prefill: %lld work-groups exceed the grid limit",
+                  (long long)blocks);
+  }
   const bool paged = block_table != nullptr;
   if (paged) {
     TMOPT_REQUIRE(k_pool && v_pool && page_size > 0 && bt_stride > 0 &&

@@ -48,12 +48,62 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kBN = 64;                   // keys per tile
-constexpr int kKRow = 272;                // K tile row: 256 B + 16 B pad
-constexpr int kVRow = 144;                // V^T tile row: 128 B + 16 B pad
-constexpr int kKBytes = kBN * kKRow;      // 17408
-constexpr int kVBytes = kD * kVRow;       // 18432
-constexpr int kStage = kKBytes + kVBytes; // 35840; two stages per block
+constexpr int kRowB = 256;                // K / V tile row in LDS (one key)
+constexpr int kTileB = kBN * kRowB;       // 16384
+constexpr int kStage = 2 * kTileB;        // K tile then V tile
+constexpr int kNStage = 4;                // 128 KB of LDS per work-group
+constexpr int kPage = 16;                 // paged source: tokens per page
 constexpr float kLazy = 8.0f;             // lazy-rescale threshold (log2)
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+// raw buffer resource: base, byte range, dword 3 as for every buffer access
+// in this library
+// (all fields are wave-uniform; readfirstlane keeps them in scalar
+// registers, as the instruction needs, even where the compiler computed a
+// field with vector instructions)
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)(uintptr_t)base;
+  return i32x4{__builtin_amdgcn_readfirstlane((int)(uint32_t)p),
+               __builtin_amdgcn_readfirstlane(
+                   (int)((uint32_t)(p >> 32) & 0xffffu)),
+               __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l of the
+// wave writes bytes lds + 16 l .. +15. Issued from inline assembly so that
+// the compiler does not wait for it at every barrier; the kernel waits for
+// these loads itself (wait_vm).
+__device__ __forceinline__ void dma_b128(i32x4 rsrc, uint32_t lds, int voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(lds), "v"(voff), "s"(rsrc)
+      : "memory");
+}
+
+// wait until at most N vector-memory loads of this wave are in flight
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) |
+                             (15 << 8));
+}
+
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+__device__ __forceinline__ bf16x8 lds_b128(uint32_t addr) {
+  return __builtin_bit_cast(bf16x8, *(const lds_u32x4*)(uintptr_t)addr);
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+// i % 4 of the 8-byte chunks addressed by lanes 4j + i / 4 (j = 0..3)
+__device__ __forceinline__ bf16x4 lds_tr16(uint32_t addr) {
+  return __builtin_bit_cast(
+      bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)addr));
+}
 
 struct PrefillArgs {
   const __bf16* q;
@@ -82,19 +132,6 @@ struct PrefillArgs {
   int64_t r_st, r_sh;
   int rel_extent;
 };
-
-// LDS column of key kappa (0..63) in a V^T row: within each 16-key chunk the
-// keys 4a+c go to 8*(a&1) + 4*(a>>1) + c, so that lane half h of the P.V
-// MFMA finds its eight keys {4h+c, 8+4h+c} in columns 8h..8h+7.
-__device__ __forceinline__ int vt_col(int kappa) {
-  const int o = kappa & 15;
-  return (kappa & ~15) + 8 * ((o >> 2) & 1) + 4 * (o >> 3) + (o & 3);
-}
-
-// byte offset of (row d, logical 16-byte chunk ch, byte-in-chunk b) in V^T
-__device__ __forceinline__ int vt_off(int d, int ch, int b) {
-  return d * kVRow + ((ch ^ ((d >> 3) & 7)) << 4) + b;
-}
 
 __device__ __forceinline__ int wave_sum(int v) {
 #pragma unroll
@@ -175,14 +212,15 @@ __device__ __forceinline__ Work schedule(const PrefillArgs& a, int BQ,
   return w;  // not reached for i < total
 }
 
-template <int REP, bool REL>
+template <int REP, bool REL, bool PAGED>
 __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   constexpr int BQ = 256 / REP;   // queries per work-group
   constexpr int QSUB = BQ / 32;   // 32-query sub-blocks per head
   extern __shared__ __align__(16) char smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;         // 8 waves: one 32-row block each
+  // 8 waves, one 32-row block each (wave index kept in a scalar register)
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int h2 = lane >> 5;       // lane half
   const Work wk = schedule(a, BQ, lane);
@@ -203,7 +241,6 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   k_lo = (k_lo / kBN) * kBN;
   const int k_hi = pos_hi + 1;                // exclusive
   const int ntiles = (k_hi - k_lo + kBN - 1) / kBN;
-  const bool paged = a.bt != nullptr;
 
   // ---- this wave's row block: head and 32-query sub-block ----------------
   const int head = kvh * REP + w / QSUB;
@@ -224,158 +261,118 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     }
   }
 
-  // ---- tile loaders (global -> registers -> LDS) -------------------------
-  // K: thread t stages keys (t>>4) + 32i (i = 0, 1), 16-byte chunk t & 15.
-  // V: thread t stages keys 2*(t>>4) + i (i = 0, 1), dims 8*(t & 15)..+7.
-  // The loads of tile j+1 are issued before tile j's math and consumed only
-  // by the LDS stores after it, so nothing may look at the loaded values in
-  // between (a select on them would make every load complete on the spot).
-  // Packed source: buffer loads over the run's rows; keys past the run fall
-  // outside the resource and read as zero. Paged source: global loads with
-  // a clamped address; the validity bits are applied at store time.
-  const int kc = tid & 15;
-  const int kr = tid >> 4;                    // 0..31
-  u32x4 kreg[2], vreg[2];
-  unsigned okbits = 0xf;
-  // (paged launches pass no k / v: their resources are empty and unused)
-  const char* kb0 = paged ? nullptr : reinterpret_cast<const char*>(
-      a.k + (int64_t)t0 * a.k_st + (int64_t)kvh * a.k_sh);
-  const char* vb0 = paged ? nullptr : reinterpret_cast<const char*>(
-      a.v + (int64_t)t0 * a.v_st + (int64_t)kvh * a.v_sh);
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<char*>(kb0), (short)0,
-      paged ? 0 : (int)(((int64_t)(len - 1) * a.k_st + kD) * 2), 0x00020000);
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<char*>(vb0), (short)0,
-      paged ? 0 : (int)(((int64_t)(len - 1) * a.v_st + kD) * 2), 0x00020000);
-  const int kst_b = (int)(a.k_st * 2), vst_b = (int)(a.v_st * 2);
-  const int koff[2] = {kr * kst_b + 16 * kc, (kr + 32) * kst_b + 16 * kc};
-  const int voff[2] = {2 * kr * vst_b + 16 * kc, (2 * kr + 1) * vst_b + 16 * kc};
+  // ---- tile loads: global -> LDS directly (buffer_load ... lds) ----------
+  // Wave w moves key rows 4w..4w+3 and 32+4w..32+4w+3 of the K and the V
+  // tile: one 1 KB instruction per 4 rows, lane l writing LDS bytes
+  // 16l..16l+15 of the 4-row block, i.e. row l>>4, physical 16-byte slot
+  // l&15. The lane fetches the logical chunk that belongs in that slot:
+  // K: slot c ^ (row & 15); V: 64-byte block b ^ (row & 3).
+  // Rows past the run end (and pages outside the pool) fall outside the
+  // buffer resource and arrive as zeros; tile offsets ride in the lane
+  // offset, which is what the hardware range-checks.
+  const int grp = lane >> 4, slot = lane & 15;
+  const int kchunk = slot ^ ((4 * w + grp) & 15);
+  const int vchunk = ((((slot >> 2) ^ grp) & 3) << 2) | (slot & 3);
+  // LDS byte address of the dynamic shared block (0 here: the kernel has
+  // no static LDS), a multiple of 256 as the fragment addressing assumes
+  const uint32_t lds0 =
+      (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)smem);
+  i32x4 rk = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
+  int kst_b = 0, vst_b = 0, klane = 0, vlane = 0;
+  [[maybe_unused]] const int row_b = a.HKV * kD * 2;   // paged: token row
+  [[maybe_unused]] const int64_t page_b = (int64_t)kPage * row_b;
+  if constexpr (!PAGED) {
+    kst_b = (int)(a.k_st * 2);
+    vst_b = (int)(a.v_st * 2);
+    rk = make_rsrc(a.k + (int64_t)t0 * a.k_st + (int64_t)kvh * a.k_sh,
+                   (uint32_t)(((int64_t)(len - 1) * a.k_st + kD) * 2));
+    rv = make_rsrc(a.v + (int64_t)t0 * a.v_st + (int64_t)kvh * a.v_sh,
+                   (uint32_t)(((int64_t)(len - 1) * a.v_st + kD) * 2));
+    klane = grp * kst_b + 16 * kchunk;
+    vlane = grp * vst_b + 16 * vchunk;
+  } else {
+    klane = grp * row_b + kvh * (kD * 2) + 16 * kchunk;
+    vlane = grp * row_b + kvh * (kD * 2) + 16 * vchunk;
+  }
+  [[maybe_unused]] const int32_t __attribute__((address_space(4)))* trow =
+      PAGED ? as_const(a.bt) + (int64_t)seq * a.bt_stride : nullptr;
+  [[maybe_unused]] const int last_lp = (nk - 1) >> 4;
 
-  // page of tile-local key kl (0..63) among the tile's 4 pages, fetched
-  // once per tile with wave-uniform scalar loads (a per-lane table load
-  // would have to complete before the K/V loads it addresses)
-  const int last_lp = (nk - 1) / a.page_size;
-  auto paged_row = [&](int p0, int p1, int p2, int p3, int kt, int kl,
-                       const __bf16* pool, bool& ok) {
-    const int kappa = kt + kl;
-    ok = kappa < nk;
-    int pg = p0;
-    pg = (kl >> 4) == 1 ? p1 : pg;
-    pg = (kl >> 4) == 2 ? p2 : pg;
-    pg = (kl >> 4) == 3 ? p3 : pg;
-    if ((unsigned)pg >= (unsigned)a.num_pages) { ok = false; pg = 0; }
-    const int64_t row = (int64_t)pg * a.page_size + (kappa % a.page_size);
-    return pool + (row * a.HKV + kvh) * kD + 8 * kc;
-  };
-
-  auto load_tile = [&](int kt) {
-    if (!paged) {
-      // per-thread offsets are loop-invariant; the tile offset rides in the
-      // scalar soffset field
+  // issue tile `t` (index from k_lo) into LDS stage `st`: 4 instructions
+  auto issue_tile = [&](int t, int st) {
+    const int kt = k_lo + t * kBN;
+    const uint32_t sb = lds0 + st * kStage;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        kreg[i] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       rk, koff[i], kt * kst_b, 0));
-        vreg[i] = __builtin_bit_cast(
-            u32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                       rv, voff[i], kt * vst_b, 0));
+    for (int i = 0; i < 2; ++i) {
+      const int r0 = 4 * w + 32 * i;          // first row of the block
+      const uint32_t dk = sb + r0 * kRowB, dv = dk + kTileB;
+      if constexpr (!PAGED) {
+        dma_b128(rk, dk, klane + (kt + r0) * kst_b);
+        dma_b128(rv, dv, vlane + (kt + r0) * vst_b);
+      } else {
+        // the 4 rows lie in one page; its resource covers only the rows
+        // of the run (and nothing for a page id outside the pool)
+        const int key0 = kt + r0;
+        const int lp = key0 >> 4;
+        const int pg = lp <= last_lp ? trow[lp] : -1;
+        const bool valid = (unsigned)pg < (unsigned)a.num_pages;
+        const int rows = min(kPage, max(0, nk - kPage * lp));
+        const uint32_t nrec = valid ? (uint32_t)(rows * row_b) : 0u;
+        const int64_t pofs = valid ? (int64_t)pg * page_b : 0;
+        const int roff = (key0 & (kPage - 1)) * row_b;
+        dma_b128(make_rsrc(reinterpret_cast<const char*>(a.kpool) + pofs,
+                           nrec),
+                 dk, klane + roff);
+        dma_b128(make_rsrc(reinterpret_cast<const char*>(a.vpool) + pofs,
+                           nrec),
+                 dv, vlane + roff);
       }
-    } else {
-      const int32_t __attribute__((address_space(4)))* trow =
-          as_const(a.bt) + (int64_t)seq * a.bt_stride;
-      const int lp0 = kt / a.page_size;
-      const int p0 = trow[min(lp0, last_lp)];
-      const int p1 = trow[min(lp0 + 1, last_lp)];
-      const int p2 = trow[min(lp0 + 2, last_lp)];
-      const int p3 = trow[min(lp0 + 3, last_lp)];
-      unsigned bits = 0;
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        bool ok;
-        const __bf16* src =
-            paged_row(p0, p1, p2, p3, kt, kr + 32 * i, a.kpool, ok);
-        kreg[i] = *reinterpret_cast<const u32x4*>(src);
-        bits |= ok ? (1u << i) : 0u;
-        src = paged_row(p0, p1, p2, p3, kt, 2 * kr + i, a.vpool, ok);
-        vreg[i] = *reinterpret_cast<const u32x4*>(src);
-        bits |= ok ? (4u << i) : 0u;
-      }
-      okbits = bits;
     }
   };
 
-  auto store_tile = [&](int stage) {
-    char* ks = smem + stage * kStage;
-    char* vs = ks + kKBytes;
-    const u32x4 z = u32x4{0, 0, 0, 0};
+  // ---- LDS fragment addresses -------------------------------------------
+  // K fragment (kb, kk) of lane (l32, h2): row 32 kb + l32, logical chunk
+  // 2 kk + h2 -> slot (2 kk + h2) ^ (l32 & 15) = (h2 ^ (l32 & 15)) ^ 2 kk.
+  const uint32_t ka0 = (uint32_t)(l32 * kRowB + 16 * (h2 ^ (l32 & 15)));
+  // V^T fragment (db, kb, kk) by two transposed reads: within each 16-lane
+  // group, source lane s names key kbase + (s >> 2), dims 4 (s & 3)..+3 of
+  // a 16-dim half; lane i of the group then holds dim dbase + i of keys
+  // kbase..kbase+3. kbase = 32 kb + 16 kk + 4 h2 (+8 for the second read),
+  // dbase = 32 db + 16 (l32 >> 4), which matches the order of this lane's
+  // probabilities (keys 16 kk + 4 h2 + 0..3 and 16 kk + 8 + 4 h2 + 0..3).
+  const int s16 = lane & 15;
+  const uint32_t va0 = (uint32_t)((4 * h2 + (s16 >> 2)) * kRowB +
+                                  64 * (s16 >> 2) + 32 * ((lane >> 4) & 1) +
+                                  8 * (s16 & 3));
+
+  // S^T = K.Q^T for the tile in `stage` (keys on M, queries on N)
+  auto scores = [&](int stage, f32x16 (&s)[2]) {
+    const uint32_t kb0 = ka0 + lds0 + stage * kStage;
+    s[0] = f32x16{};
+    s[1] = f32x16{};
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      *reinterpret_cast<u32x4*>(ks + (kr + 32 * i) * kKRow + 16 * kc) =
-          (okbits & (1u << i)) ? kreg[i] : z;
-    const u32x4 v0 = (okbits & 4u) ? vreg[0] : z;
-    const u32x4 v1 = (okbits & 8u) ? vreg[1] : z;
-    // V^T: dims 8kc+e, keys 2kr, 2kr+1 -> one 4-byte write per dim
-    const int col = vt_col(2 * kr);
-    const int ch = col >> 3;          // 16-byte chunk (8 keys)
-    const int b = (col & 7) * 2;
+    for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int d = 8 * kc + 2 * c;
-      *reinterpret_cast<uint32_t*>(vs + vt_off(d, ch, b)) =
-          interleave_lo(v0[c], v1[c]);
-      *reinterpret_cast<uint32_t*>(vs + vt_off(d + 1, ch, b)) =
-          interleave_hi(v0[c], v1[c]);
-    }
+      for (int kb = 0; kb < 2; ++kb) {
+        const bf16x8 kf = lds_b128((kb0 ^ (32u * kk)) + 32 * kb * kRowB);
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kb], 0,
+                                                        0, 0);
+      }
   };
 
-  // ---- accumulators -----------------------------------------------------
-  f32x16 o_acc[4];
-#pragma unroll
-  for (int db = 0; db < 4; ++db) o_acc[db] = f32x16{};
-  float m_run = -INFINITY;
-  float l_part = 0.0f;
+  // V^T fragment (db, kb, kk) of the tile whose V rows start at vbase
+  auto vfrag = [&](uint32_t vdb, int kb, int kk) {
+    const uint32_t p = vdb + (32 * kb + 16 * kk) * kRowB;
+    const bf16x4 lo = lds_tr16(p);
+    const bf16x4 hi = lds_tr16(p + 8 * kRowB);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
 
-  load_tile(k_lo);
-  store_tile(0);
-  __syncthreads();
-
-  for (int it = 0; it < ntiles; ++it) {
-    const int kt = k_lo + it * kBN;
-    const int stage = it & 1;
-    if (it + 1 < ntiles) load_tile(kt + kBN);
-    const char* ks = smem + stage * kStage;
-    const char* vs = ks + kKBytes;
-
-    // does any element of this tile need masking?
-    const bool full = (kt + kBN - 1 <= pos_lo) && (kt + kBN <= nk) &&
-                      (a.window == 0 || pos_hi - kt < a.window) &&
-                      (qn == BQ);
-
-    // ---- S^T = K.Q^T ----------------------------------------------------
-    f32x16 sc[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      sc[kb] = f32x16{};
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        const bf16x8 kf = __builtin_bit_cast(
-            bf16x8, *reinterpret_cast<const u32x4*>(
-                        ks + (32 * kb + l32) * kKRow + 32 * kk + 16 * h2));
-        sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], sc[kb],
-                                                         0, 0, 0);
-      }
-    }
-
-    // ---- online softmax -------------------------------------------------
-    // Without a bias the max runs on the raw scores (scale > 0 commutes with
-    // max) and each probability is one fma + exp2: p = 2^(s*scale*log2e - m).
-    // With the fused relative bias (attn_prefill.py:115-120) the scores are
-    // first moved to the log2 domain, s*scale*log2e + rel*log2e, gathered at
-    // rel[q, h, dist] for 0 <= dist < E and zero outside the band.
-    float sl2 = a.scale_log2;
+  // per-element mask (causal, window, run end) and optional fused bias
+  auto mask_bias = [&](f32x16 (&s)[2], int kt) {
     if constexpr (REL) {
+      // the scores move to the log2 domain: s*scale*log2e + rel*log2e,
+      // rel gathered at rel[q, h, dist] for 0 <= dist < E, zero outside
       const __bf16* rrow = a.rel + (int64_t)(t0 + (qok ? qi : 0)) * a.r_st +
                            (int64_t)head * a.r_sh;
 #pragma unroll
@@ -386,83 +383,246 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
           const int dist = qpos - kp;
           const bool band = qok && dist >= 0 && dist < a.rel_extent;
           const float bias = band ? (float)rrow[dist] : 0.0f;
-          sc[kb][j] = __builtin_fmaf(sc[kb][j], a.scale_log2, bias * kLog2e);
-        }
-      sl2 = 1.0f;
-    }
-    if (!full) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int kp = kt + 32 * kb + 8 * (j >> 2) + 4 * h2 + (j & 3);
-          const int dist = qpos - kp;
-          const bool ok = qok && dist >= 0 && kp < nk &&
-                          (a.window == 0 || dist < a.window);
-          sc[kb][j] = ok ? sc[kb][j] : -INFINITY;
+          s[kb][j] = __builtin_fmaf(s[kb][j], a.scale_log2, bias * kLog2e);
         }
     }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int kp = kt + 32 * kb + 8 * (j >> 2) + 4 * h2 + (j & 3);
+        const int dist = qpos - kp;
+        const bool ok = qok && dist >= 0 && kp < nk &&
+                        (a.window == 0 || dist < a.window);
+        s[kb][j] = ok ? s[kb][j] : -INFINITY;
+      }
+  };
+
+  // ---- accumulators -----------------------------------------------------
+  f32x16 o_acc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) o_acc[db] = f32x16{};
+  float m_run = -INFINITY;
+  float l_part = 0.0f;
+  // Without a bias the max runs on the raw scores (scale > 0 commutes with
+  // max) and each probability is one fma + exp2: p = 2^(s*scale*log2e - m).
+  const float sl2 = REL ? 1.0f : a.scale_log2;
+
+  // Lazy rescaling: the running max (log2 domain) only moves when the
+  // tile's max exceeds it by more than kLazy, so probabilities stay below
+  // 2^kLazy and O^T / l are rescaled on few tiles; O / l and the LSE are
+  // exact for any reference point.
+  auto new_max = [&](float mx, bool& move, float& m_use) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(
+        __builtin_bit_cast(uint32_t, mx), __builtin_bit_cast(uint32_t, mx),
+        false, false);
+    mx = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]),
+               __builtin_bit_cast(float, (uint32_t)sw[1]));
+    const float m_cand = mx * sl2;
+    move = m_cand > m_run + kLazy;
+    const float m_new = move ? m_cand : m_run;
+    m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = move ? fast_exp2(m_run - m_use) : 1.0f;
+    m_run = m_new;
+    return alpha;
+  };
+  // probability pair q (kb = q >> 3, kk = (q >> 2) & 1, e = q & 3)
+  auto prob_pair = [&](const f32x16 (&s)[2], int q, float m_use,
+                       float& psum) {
+    const int kb = q >> 3, kk = (q >> 2) & 1, e = q & 3;
+    const float p0 =
+        fast_exp2(__builtin_fmaf(s[kb][8 * kk + 2 * e], sl2, -m_use));
+    const float p1 =
+        fast_exp2(__builtin_fmaf(s[kb][8 * kk + 2 * e + 1], sl2, -m_use));
+    psum += p0 + p1;
+    return pack_bf16x2_rn(p0, p1);
+  };
+  auto pack_p = [&](const uint32_t (&pw)[16], bf16x8 (&pf)[2][2]) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int q = 8 * kb + 4 * kk;
+        pf[kb][kk] = __builtin_bit_cast(
+            bf16x8, u32x4{pw[q], pw[q + 1], pw[q + 2], pw[q + 3]});
+      }
+  };
+
+  // The softmax of a tile is done in two halves so that neither MFMA phase
+  // runs alone: half 1 (max, reference point, probability pairs 0..7) runs
+  // under the previous tile's P.V MFMAs, half 2 (pairs 8..15) under the
+  // next tile's score MFMAs, about five VALU instructions per MFMA in
+  // both phases.
+  struct Soft {
+    float alpha, m_use, psum;
+    bool move;
+    uint32_t pw[16];
+  };
+  auto tile_max = [&](const f32x16 (&s)[2]) {
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int j = 0; j < 16; j += 2)
-        mx = fmaxf(fmaxf(mx, sc[kb][j]), sc[kb][j + 1]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    // Lazy rescaling: the running max (log2 domain) only moves when the
-    // tile's max exceeds it by more than kLazy, so probabilities stay below
-    // 2^kLazy and O^T / l are rescaled on few tiles; O / l and the LSE are
-    // exact for any reference point.
-    const float m_cand = mx * sl2;
-    const bool move = m_cand > m_run + kLazy;
-    const float m_new = move ? m_cand : m_run;
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = move ? fast_exp2(m_run - m_use) : 1.0f;
-    m_run = m_new;
-    float psum = 0.0f;
-    bf16x8 pf[2][2];  // [kb][kk]
+        mx = fmaxf(fmaxf(mx, s[kb][j]), s[kb][j + 1]);
+    return mx;
+  };
+  // half 1 without interleave (masked / biased tiles, the first tile)
+  auto half1_plain = [&](const f32x16 (&s)[2], Soft& sf) {
+    sf.alpha = new_max(tile_max(s), sf.move, sf.m_use);
+    sf.psum = 0.0f;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int q = 0; q < 8; ++q) sf.pw[q] = prob_pair(s, q, sf.m_use, sf.psum);
+  };
+  auto half2_plain = [&](const f32x16 (&s)[2], Soft& sf) {
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        uint32_t pw[4];
+    for (int q = 8; q < 16; ++q) sf.pw[q] = prob_pair(s, q, sf.m_use, sf.psum);
+  };
+
+  // Phase A of tile it: the next tile's scores (16 MFMAs, K fragments read
+  // three chunks ahead) with half 2 of this tile's softmax between them,
+  // chunk by chunk. A scheduling fence after every chunk keeps the
+  // interleave, and each chunk's results are pinned in place by an empty
+  // asm that takes them as operands (pure arithmetic would otherwise be
+  // sunk to its first use, past the fences, before scheduling starts).
+  auto front = [&](int st_n, const f32x16 (&cur)[2], f32x16 (&nxt)[2],
+                   Soft& sf) {
+    const uint32_t kb0 = ka0 + lds0 + st_n * kStage;
+    auto kfrag = [&](int n) {
+      return lds_b128((kb0 ^ (32u * (n >> 1))) + 32 * (n & 1) * kRowB);
+    };
+    bf16x8 kf[4];
+    kf[0] = kfrag(0);
+    kf[1] = kfrag(1);
+    kf[2] = kfrag(2);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p0 = fast_exp2(
-              __builtin_fmaf(sc[kb][8 * kk + 2 * e], sl2, -m_use));
-          const float p1 = fast_exp2(
-              __builtin_fmaf(sc[kb][8 * kk + 2 * e + 1], sl2, -m_use));
-          psum += p0 + p1;
-          pw[e] = pack_bf16x2_rn(p0, p1);
-        }
-        pf[kb][kk] =
-            __builtin_bit_cast(bf16x8, u32x4{pw[0], pw[1], pw[2], pw[3]});
+    for (int n = 0; n < 16; ++n) {
+      if (n + 3 < 16) kf[(n + 3) & 3] = kfrag(n + 3);
+      const int kb = n & 1, kk = n >> 1;
+      nxt[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          kf[n & 3], qf[kk], n < 2 ? f32x16{} : nxt[kb], 0, 0, 0);
+      if (n & 1) {
+        const int q = 8 + (n >> 1);
+        sf.pw[q] = prob_pair(cur, q, sf.m_use, sf.psum);
+        asm volatile("" : "+v"(sf.pw[q]), "+v"(sf.psum));
       }
-    l_part = l_part * alpha + psum;
-    // rescale O^T only when some lane's reference point moved
-    if (__builtin_amdgcn_ballot_w64(move)) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db) o_acc[db] = o_acc[db] * alpha;
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
 
-    // ---- O^T += V^T.P^T --------------------------------------------------
+  // Phase B of tile it: O^T += V^T.P^T (16 MFMAs, V^T fragments read three
+  // ahead, the four accumulators in turn) with half 1 of the next tile's
+  // softmax between them: the max over chunks 0..3, the reference point in
+  // chunk 4, pairs 0..7 over chunks 5..15.
+  auto back = [&](int stage, const bf16x8 (&pf)[2][2],
+                  const f32x16 (&nxt)[2], Soft& sn, bool with_next) {
+    const uint32_t vb = va0 + lds0 + stage * kStage + kTileB;
+    auto vf_n = [&](int n) {
+      const int db = n & 3, kb = n >> 3, kk = (n >> 2) & 1;
+      return vfrag(vb ^ (64u * db), kb, kk);
+    };
+    bf16x8 vf[4];
+    vf[0] = vf_n(0);
+    vf[1] = vf_n(1);
+    vf[2] = vf_n(2);
+    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      const int d = 32 * db + l32;
+    for (int n = 0; n < 16; ++n) {
+      if (n + 3 < 16) vf[(n + 3) & 3] = vf_n(n + 3);
+      const int db = n & 3, kb = n >> 3, kk = (n >> 2) & 1;
+      o_acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          vf[n & 3], pf[kb][kk], o_acc[db], 0, 0, 0);
+      if (with_next) {
+        if (n < 4) {
+          const int kb2 = n >> 1, j0 = 8 * (n & 1);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+          for (int j = 0; j < 8; j += 2)
+            mx[n] = fmaxf(fmaxf(mx[n], nxt[kb2][j0 + j]), nxt[kb2][j0 + j + 1]);
+          asm volatile("" : "+v"(mx[n]));
+        } else if (n == 4) {
+          sn.alpha = new_max(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])),
+                             sn.move, sn.m_use);
+          sn.psum = 0.0f;
+          asm volatile("" : "+v"(sn.alpha), "+v"(sn.m_use));
+        } else {
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const bf16x8 vf = __builtin_bit_cast(
-              bf16x8, *reinterpret_cast<const u32x4*>(
-                          vs + vt_off(d, 2 * (2 * kb + kk) + h2, 0)));
-          o_acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              vf, pf[kb][kk], o_acc[db], 0, 0, 0);
+          for (int q = 0; q < 8; ++q)
+            if (5 + (q * 11) / 8 == n) {
+              sn.pw[q] = prob_pair(nxt, q, sn.m_use, sn.psum);
+              asm volatile("" : "+v"(sn.pw[q]), "+v"(sn.psum));
+            }
         }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
 
-    if (it + 1 < ntiles) store_tile(stage ^ 1);
+  auto full_tile = [&](int kt) {
+    return (kt + kBN - 1 <= pos_lo) && (kt + kBN <= nk) &&
+           (a.window == 0 || pos_hi - kt < a.window) && (qn == BQ);
+  };
+
+  // ---- pipeline: 4 LDS stages, tiles issued two ahead ---------------------
+  // At the top of step `it`, tiles it and it+1 are in LDS (published by a
+  // barrier) and tile it+2 is in flight; step it issues tile it+3 into the
+  // stage tile it-1 used, and before its closing barrier waits for tile
+  // it+2 (every wave issues 4 instructions per tile).
+  issue_tile(0, 0);
+  if (ntiles > 1) issue_tile(1, 1);
+  if (ntiles > 2) {
+    issue_tile(2, 2);
+    wait_vm<4>();
+  } else {
+    wait_vm<0>();
+  }
+  __syncthreads();
+
+  int st_cur = 0;   // stage of tile it
+  Soft sf;          // softmax state of tile it (half 1 done)
+  auto step = [&](int it, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
+    const int kt = k_lo + it * kBN;
+    const int st_nxt = (st_cur + 1) & 3;
+    const bool has_next = it + 1 < ntiles;
+    // phase A: rescale O^T if some lane's reference point moved, then the
+    // next tile's scores under half 2 of this tile's softmax
+    if (__builtin_amdgcn_ballot_w64(sf.move)) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o_acc[db] = o_acc[db] * sf.alpha;
+    }
+    if (!REL && has_next) {
+      front(st_nxt, cur, nxt, sf);
+    } else {
+      half2_plain(cur, sf);
+      if (has_next) scores(st_nxt, nxt);
+    }
+    bf16x8 pf[2][2];
+    pack_p(sf.pw, pf);
+    l_part = l_part * sf.alpha + sf.psum;
+    // phase B: P.V of this tile under half 1 of the next tile's softmax
+    const bool more = it + 3 < ntiles;
+    if (more) issue_tile(it + 3, (st_cur + 3) & 3);
+    if (has_next && !REL && full_tile(kt + kBN)) {
+      back(st_cur, pf, nxt, sf, true);
+    } else {
+      back(st_cur, pf, nxt, sf, false);
+      if (has_next) {
+        mask_bias(nxt, kt + kBN);
+        half1_plain(nxt, sf);
+      }
+    }
+    if (more) wait_vm<4>(); else wait_vm<0>();
     __syncthreads();
+    st_cur = st_nxt;
+  };
+
+  f32x16 sa[2], sb[2];
+  scores(0, sa);
+  if (REL || !full_tile(k_lo)) mask_bias(sa, k_lo);
+  half1_plain(sa, sf);
+  for (int it = 0; it < ntiles; ++it) {
+    step(it, sa, sb);
+    sa[0] = sb[0];
+    sa[1] = sb[1];
   }
 
   // ---- finalise: l over both lane halves, normalise, store --------------
@@ -495,12 +655,23 @@ void launch(PrefillArgs a, int S, int max_seqlen, hipStream_t st) {
   int64_t n = a.HKV * items;
   if (a.HKV <= 8 && 8 % a.HKV == 0) n = 8 * ((items + 8 / a.HKV - 1) / (8 / a.HKV));
   dim3 grid((unsigned)n);
-  if (a.rel)
-    hipLaunchKernelGGL((prefill_kernel<REP, true>), grid, dim3(512),
-                       2 * kStage, st, a);
-  else
-    hipLaunchKernelGGL((prefill_kernel<REP, false>), grid, dim3(512),
-                       2 * kStage, st, a);
+  const bool paged = a.bt != nullptr;
+  const size_t lds = kNStage * kStage;
+  if (a.rel) {
+    if (paged)
+      hipLaunchKernelGGL((prefill_kernel<REP, true, true>), grid, dim3(512),
+                         lds, st, a);
+    else
+      hipLaunchKernelGGL((prefill_kernel<REP, true, false>), grid, dim3(512),
+                         lds, st, a);
+  } else {
+    if (paged)
+      hipLaunchKernelGGL((prefill_kernel<REP, false, true>), grid, dim3(512),
+                         lds, st, a);
+    else
+      hipLaunchKernelGGL((prefill_kernel<REP, false, false>), grid,
+                         dim3(512), lds, st, a);
+  }
 }
 
 }  // namespace
@@ -549,6 +720,8 @@ extern "C" int tmopt_attn_prefill_varlen(
                       num_pages > 0,
                   TMOPT_EINVAL,
                   "prefill: paged source needs pools, page_size, bt_stride");
+    TMOPT_REQUIRE(page_size == kPage, TMOPT_EUNSUPPORTED,
+                  "prefill: page_size=%d (only 16)", page_size);
     TMOPT_REQUIRE(((uintptr_t)k_pool | (uintptr_t)v_pool) % 16 == 0,
                   TMOPT_EINVAL, "prefill: pools must be 16-byte aligned");
   } else {

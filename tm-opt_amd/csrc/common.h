@@ -73,6 +73,27 @@ as_const(const T* p) {
 // Order LDS accesses of one wave: every lane's prior LDS writes are visible
 // to every lane's later LDS reads, and the compiler may not move LDS traffic
 // across this point.
+// ---- LDS access by 32-bit LDS byte address -------------------------------
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+__device__ __forceinline__ bf16x8 lds_ld128(uint32_t addr) {
+  return __builtin_bit_cast(bf16x8, *(const lds_u32x4*)(uintptr_t)addr);
+}
+
+__device__ __forceinline__ void lds_st128(uint32_t addr, u32x4 v) {
+  *(lds_u32x4*)(uintptr_t)addr = v;
+}
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
+// i % 4 of the 8-byte chunks addressed by lanes 4j + i / 4 (j = 0..3), i.e.
+// a 4 x 16 block of 16-bit values comes back transposed
+__device__ __forceinline__ bf16x4 lds_tr16(uint32_t addr) {
+  return __builtin_bit_cast(
+      bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)addr));
+}
+
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();

@@ -51,8 +51,9 @@ namespace {
 
 constexpr int kD = 128;
 constexpr int kPS = 16;                      // tokens per page
-constexpr int kVtRowBytes = 88;              // 64 B of tokens + 24 B pad
-constexpr int kVtBytes = kD * kVtRowBytes;   // per wave
+constexpr int kRowB = 256;                   // one token's head slice
+constexpr int kTileB = 2 * kPS * kRowB;      // 32 tokens: 8 KB
+constexpr int kWaveLds = 2 * kTileB;         // K tile + V tile per wave
 constexpr int kMaxB = 8192;                  // prefix table lives in LDS
 // cache policy of the K/V page loads: non-temporal (streamed once; the
 // measured read rate of a plain stream rises from 6.2 to 6.9 TB/s with it)
@@ -120,7 +121,7 @@ struct Step {
 
 template <bool REL>
 struct StepBuf {
-  u32x4 k[2][4];  // [tile][kk]
+  u32x4 k[2][4];  // [tile][load]: tokens 16 t + 4 i + (lane >> 4)
   u32x4 v[2][4];
   // raw bf16 bias bits of this lane's 8 scores, [4t + i] for token
   // 16t + 4g + i; converted only when used, so issuing never waits
@@ -154,19 +155,23 @@ __device__ __forceinline__ void issue_step(StepBuf<REL>& buf,
             rr, off, 0, 0);
       }
   }
+  // lane l of load i reads 16 bytes of token 4i + (l >> 4): each group of
+  // 16 lanes reads one token's 256-byte head slice, so consecutive lanes
+  // are contiguous and every instruction coalesces into 64-byte requests
+  const int tok_b = page_bytes / kPS;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
     const int phys = t == 0 ? st.phys0 : st.phys1;
     __amdgpu_buffer_rsrc_t rk = page_rsrc(a.kpool, phys, page_bytes);
     __amdgpu_buffer_rsrc_t rv = page_rsrc(a.vpool, phys, page_bytes);
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      buf.k[t][kk] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, lane_off + 64 * kk,
-                                                       0, kStreamLoad));
-      buf.v[t][kk] = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, lane_off + 64 * kk,
-                                                       0, kStreamLoad));
+    for (int i = 0; i < 4; ++i) {
+      buf.k[t][i] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     rk, lane_off + 4 * i * tok_b, 0, kStreamLoad));
+      buf.v[t][i] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     rv, lane_off + 4 * i * tok_b, 0, kStreamLoad));
     }
   }
 }
@@ -183,9 +188,10 @@ void decode_kernel(DecodeArgs a) {
   const int wg = blockIdx.x;
   const int G = gridDim.x;
   const int kvh = blockIdx.y * nw + w;
-  char* vt = smem + w * kVtBytes;
-  int* pref = reinterpret_cast<int*>(smem + nw * kVtBytes);  // [B + 1]
-  int* wsum = pref + a.B + 1;                                // [4]
+  // the prefix table is only read before the walk; the per-wave K / V
+  // tiles then reuse the same LDS (a barrier separates the two uses)
+  int* pref = reinterpret_cast<int*>(smem);  // [B + 1]
+  int* wsum = pref + a.B + 1;                // [4]
 
   // ---- 1. prefix sums of visible pages: pref[b] = first unit of seq b ----
   {
@@ -282,8 +288,29 @@ void decode_kernel(DecodeArgs a) {
 
   const int row_elems = a.HKV * kD;
   const int page_bytes = kPS * row_elems * 2;
-  // byte offset of (token r, head kvh, dims 8g..) inside a page
-  const int lane_off = (r * row_elems + kvh * kD + 8 * g) * 2;
+  // byte offset of (token lane >> 4, head kvh, dims 8 (lane & 15)..) in a
+  // page
+  const int lane_off = ((lane >> 4) * row_elems + kvh * kD + 8 * (lane & 15)) * 2;
+  // this wave's LDS tiles: 32 token rows of 256 B each for K, then for V.
+  // K row x keeps 16-byte chunk c at slot c ^ (x & 15), V row x keeps
+  // 32-byte unit u at slot u ^ (x & 7): conflict-free for the row writes,
+  // for the K fragment reads (16 rows, one chunk) and for the transposed V
+  // reads (8 rows, one unit, per 32 lanes).
+  // The four lane-dependent bases below (multiples of 256 plus a swizzled
+  // slot) give every access as base ^ (slot bits) + immediate.
+  const uint32_t kt_l = (uint32_t)(uintptr_t)(
+      (__attribute__((address_space(3))) char*)smem) + w * kWaveLds;
+  const uint32_t vt_l = kt_l + kTileB;
+  const int wtok = lane >> 4, wch = lane & 15;  // row / chunk of a write
+  // write of load i, tile t: row x = 16t + 4i + wtok
+  const uint32_t kw0 = kt_l + wtok * kRowB + 16 * (wch ^ wtok);
+  const uint32_t vw0 = vt_l + wtok * kRowB + 32 * ((wch >> 1) ^ wtok) + 16 * (wch & 1);
+  // K fragment (t, kk) of lane (r, g): row 16t + r, chunk 4kk + g
+  const uint32_t kr0 = kt_l + r * kRowB + 16 * (g ^ r);
+  // transposed V reads: rows 4g + (s >> 2) (+16), unit blk, dims 4 (s & 3)
+  const int s16 = lane & 15;
+  const int x0 = 4 * g + (s16 >> 2);
+  const uint32_t vr0 = vt_l + x0 * kRowB + 32 * (x0 & 7) + 8 * (s16 & 3);
 
   // ---- per-piece state ----------------------------------------------------
   f32x4 o_acc[8];
@@ -309,6 +336,26 @@ void decode_kernel(DecodeArgs a) {
     const int n = st.n;
     const int lo = vis_lo(n, a.window);
     if (st.b != q_b) load_q(st.b);
+    // ---- stage K and V rows in LDS -----------------------------------------
+    // (V rows of invalid tokens are zeroed: masked probabilities are 0 and
+    // must not meet a NaN in P.V)
+    const int k0 = st.pg * kPS;
+    wave_lds_sync();  // the previous step's fragment reads are done
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const bool page_ok = (t == 0 ? st.phys0 : st.phys1) >= 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // row x = 16t + 4i + wtok: x & 15 = 4i ^ wtok, x & 7 = 4(i & 1) ^ wtok
+        const int kpos = k0 + 16 * t + 4 * i + wtok;
+        const bool vok = page_ok && kpos >= lo && kpos < n;
+        const uint32_t rowo = (16 * t + 4 * i) * kRowB;
+        lds_st128((kw0 ^ (64u * i)) + rowo, buf.k[t][i]);
+        lds_st128((vw0 ^ (128u * (i & 1))) + rowo,
+                  vok ? buf.v[t][i] : u32x4{0, 0, 0, 0});
+      }
+    }
+    wave_lds_sync();
     // ---- S^T = K.Q^T for the two 16-token tiles -------------------------
     f32x4 sc[2];
 #pragma unroll
@@ -317,7 +364,8 @@ void decode_kernel(DecodeArgs a) {
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk)
         sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-            __builtin_bit_cast(bf16x8, buf.k[t][kk]), qf[kk], sc[t], 0, 0, 0);
+            lds_ld128((kr0 ^ (64u * kk)) + 16 * t * kRowB), qf[kk], sc[t], 0,
+            0, 0);
     }
     // ---- mask, bias, running max ----------------------------------------
     float x[2][4];
@@ -343,46 +391,34 @@ void decode_kernel(DecodeArgs a) {
     const float alpha = fast_exp2(m_run - m_use);
     m_run = m_new;
     // ---- probabilities: fp32 sum, bf16 operand --------------------------
+    // B-operand element j = 4t + i  <->  token 16t + 4g + i
     float psum = 0.0f;
+    float p[2][4];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[t][i] = fast_exp2(x[t][i] - m_use);
+        psum += p[t][i];
+      }
+    l_part = l_part * alpha + psum;
     uint32_t pw[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float p0 = fast_exp2(x[0][i] - m_use);
-      const float p1 = fast_exp2(x[1][i] - m_use);
-      psum += p0 + p1;
-      // B-operand element j = 2i + t  <->  token 16t + 4g + i
-      pw[i] = pack_bf16x2(f32_to_bf16_bits(p0), f32_to_bf16_bits(p1));
-    }
-    l_part = l_part * alpha + psum;
+    for (int j = 0; j < 4; ++j)
+      pw[j] = pack_bf16x2(f32_to_bf16_bits(p[j >> 1][2 * (j & 1)]),
+                          f32_to_bf16_bits(p[j >> 1][2 * (j & 1) + 1]));
     const bf16x8 pf =
         __builtin_bit_cast(bf16x8, u32x4{pw[0], pw[1], pw[2], pw[3]});
-    // ---- V^T into LDS (rows of invalid tokens zeroed: NaN-safe) ---------
-    const int k0 = st.pg * kPS + r;
-    const bool v0_ok = st.phys0 >= 0 && k0 >= lo && k0 < n;
-    const bool v1_ok = st.phys1 >= 0 && k0 + kPS >= lo && k0 + kPS < n;
-    wave_lds_sync();  // previous step's V^T reads are done
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-#pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const uint32_t a0 = v0_ok ? buf.v[0][kk][c] : 0u;
-        const uint32_t a1 = v1_ok ? buf.v[1][kk][c] : 0u;
-        const int d = 32 * kk + 8 * g + 2 * c;
-        *reinterpret_cast<uint32_t*>(vt + d * kVtRowBytes + 4 * r) =
-            interleave_lo(a0, a1);
-        *reinterpret_cast<uint32_t*>(vt + (d + 1) * kVtRowBytes + 4 * r) =
-            interleave_hi(a0, a1);
-      }
-    }
-    wave_lds_sync();
     // ---- O^T = O^T * alpha + V^T.P^T ------------------------------------
+    // A operand (dims 16 blk + r, tokens 4g..4g+3 and 16+4g..16+4g+3) by two
+    // transposed reads: source lane s of each 16-lane group names token
+    // base + (s >> 2) and dims 16 blk + 4 (s & 3)..+3
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) {
-      const char* src = vt + (16 * blk + r) * kVtRowBytes + 16 * g;
-      const u32x2 lo2 = *reinterpret_cast<const u32x2*>(src);
-      const u32x2 hi2 = *reinterpret_cast<const u32x2*>(src + 8);
-      const bf16x8 vf =
-          __builtin_bit_cast(bf16x8, u32x4{lo2[0], lo2[1], hi2[0], hi2[1]});
+      const uint32_t va = vr0 ^ (32u * blk);
+      const bf16x4 lo4 = lds_tr16(va);
+      const bf16x4 hi4 = lds_tr16(va + 16 * kRowB);
+      const bf16x8 vf = __builtin_shufflevector(lo4, hi4, 0, 1, 2, 3, 4, 5, 6, 7);
       o_acc[blk] = o_acc[blk] * alpha;
       o_acc[blk] =
           __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o_acc[blk], 0, 0, 0);
@@ -430,6 +466,8 @@ void decode_kernel(DecodeArgs a) {
     m_run = -INFINITY;
     l_part = 0.0f;
   };
+
+  __syncthreads();  // every wave is done with the prefix table
 
   // ---- 4. software-pipelined walk: next step's loads fly during math ----
   StepBuf<REL> A, B;
@@ -641,7 +679,9 @@ extern "C" int tmopt_attn_decode_paged(
   a.geo = (int*)((char*)workspace + off_geo);
 
   const int nw = waves_per_wg(HKV);
-  const size_t lds = (size_t)nw * kVtBytes + ((size_t)B + 1 + 4) * sizeof(int);
+  const size_t tab = ((size_t)B + 1 + 4) * sizeof(int);
+  const size_t tiles = (size_t)nw * kWaveLds;
+  const size_t lds = tab > tiles ? tab : tiles;
   hipStream_t st = (hipStream_t)stream;
   switch (rep) {
     case 1: launch<1>(a, G, nw, lds, st); break;

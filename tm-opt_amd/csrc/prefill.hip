@@ -56,7 +56,6 @@ constexpr int kPage = 16;                 // paged source: tokens per page
 constexpr float kLazy = 8.0f;             // lazy-rescale threshold (log2)
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 // raw buffer resource: base, byte range, dword 3 as for every buffer access
 // in this library
@@ -89,20 +88,6 @@ __device__ __forceinline__ void wait_vm() {
   static_assert(N >= 0 && N < 64, "vmcnt");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) |
                              (15 << 8));
-}
-
-typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
-
-__device__ __forceinline__ bf16x8 lds_b128(uint32_t addr) {
-  return __builtin_bit_cast(bf16x8, *(const lds_u32x4*)(uintptr_t)addr);
-}
-
-// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
-// i % 4 of the 8-byte chunks addressed by lanes 4j + i / 4 (j = 0..3)
-__device__ __forceinline__ bf16x4 lds_tr16(uint32_t addr) {
-  return __builtin_bit_cast(
-      bf16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)addr));
 }
 
 struct PrefillArgs {
@@ -354,7 +339,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 kf = lds_b128((kb0 ^ (32u * kk)) + 32 * kb * kRowB);
+        const bf16x8 kf = lds_ld128((kb0 ^ (32u * kk)) + 32 * kb * kRowB);
         s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kb], 0,
                                                         0, 0);
       }
@@ -489,7 +474,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
                    Soft& sf) {
     const uint32_t kb0 = ka0 + lds0 + st_n * kStage;
     auto kfrag = [&](int n) {
-      return lds_b128((kb0 ^ (32u * (n >> 1))) + 32 * (n & 1) * kRowB);
+      return lds_ld128((kb0 ^ (32u * (n >> 1))) + 32 * (n & 1) * kRowB);
     };
     bf16x8 kf[4];
     kf[0] = kfrag(0);

@@ -10,8 +10,9 @@
 //    end to end (U pages in total) and work-group i of G processes the
 //    contiguous range [i*C, (i+1)*C), C = max(ceil(U / G), min_pages). Every
 //    work-group therefore streams the same number of bytes whatever the
-//    length distribution, and the grid is fixed (G = 2 per CU), so one
-//    launch shape serves every step of a captured hipGraph.
+//    length distribution, and the grid is fixed (G = 3/4 of the CUs by
+//    default), so one launch shape serves every step of a captured
+//    hipGraph.
 //  * Only pages holding visible keys are touched: [lo/16, ceil(n/16)) where
 //    lo = max(0, n - window) on sliding-window layers, 0 on global ones.
 //  * A sequence cut by work-group boundaries leaves one normalised partial
@@ -27,23 +28,29 @@
 //    whole 16 KB pages. K and V arrive by 16-byte buffer loads whose
 //    resource is one page: a missing page (past the range, or a table entry
 //    outside the pool) has zero records, so its loads return zeros without
-//    touching memory, and the next step's loads are always issued before
-//    the current step's math (no branch around them, no vmcnt(0) drain).
+//    touching memory, and the next step's loads (query rows included, when
+//    the step starts a new sequence) are always issued before the current
+//    step's math (no branch around them, no vmcnt(0) drain).
+//  * Coalesced loads: each group of 16 lanes reads one token's 256-byte
+//    head slice (lanes 16 B apart); the rows are then staged through a
+//    per-wave LDS tile (XOR-swizzled: conflict-free on 64 banks) from which
+//    the MFMA fragments are read, V by transposed reads. Loading the MFMA
+//    layout directly (16 tokens per instruction, lanes 1 KB apart) cost
+//    12-15 % of the bandwidth.
 //  * Scores and P.V run on MFMA (v_mfma_f32_16x16x32_bf16). S^T = K.Q^T puts
 //    16 tokens on the M axis and the REP heads (padded to 16) on N, so each
 //    lane owns 8 scores of one head: the running max needs two cross-lane
 //    steps (xor 16, xor 32) and the running sum stays lane-local until the
 //    end of a piece. P^T is then already in the B-operand layout of
-//    O^T = V^T.P^T; V^T comes from a per-wave LDS tile written transposed
-//    (two tokens packed per dword).
+//    O^T = V^T.P^T.
 //
 // Per step (two pages = 32 tokens, tile t = page t):
-//  K tile t, MFMA row r <- token 16t + r; lane (r, g) loads dims 32kk+8g..+7.
-//  V: lane (r, g) loads tokens r and 16 + r of the same dims and writes the
-//  pair (V[r][d], V[16+r][d]) as one dword at LDS column pair 2r of row d.
-//  Column c of the V^T tile therefore holds token 16*(c&1) + (c>>1), and
-//  lane (r, g) of the P.V MFMA reads columns 8g..8g+7 (16 bytes), i.e.
-//  tokens 4g+i (t = 0) and 16+4g+i (t = 1), matching the P^T lane layout.
+//  Load i of tile t brings tokens 16t + 4i + (lane >> 4), 16 bytes (dims
+//  8 (lane & 15)..+7) per lane, into LDS rows of 256 B.
+//  S^T: lane (r, g) reads row 16t + r, dims 32kk + 8g..+7 (one 16-byte read).
+//  P.V: the A operand of lane (r, g) is dim 16 blk + r of tokens 4g..4g+3
+//  and 16+4g..16+4g+3 (two transposed reads), matching the P^T lane layout
+//  (element 4t + i <-> token 16t + 4g + i).
 #include "common.h"
 
 namespace tmopt {
@@ -54,6 +61,10 @@ constexpr int kPS = 16;                      // tokens per page
 constexpr int kRowB = 256;                   // one token's head slice
 constexpr int kTileB = 2 * kPS * kRowB;      // 32 tokens: 8 KB
 constexpr int kWaveLds = 2 * kTileB;         // K tile + V tile per wave
+#ifndef TMOPT_DECODE_DEEP
+#define TMOPT_DECODE_DEEP 2
+#endif
+constexpr int kDeep = TMOPT_DECODE_DEEP;     // step ring depth
 constexpr int kMaxB = 8192;                  // prefix table lives in LDS
 // cache policy of the K/V page loads: non-temporal (streamed once; the
 // measured read rate of a plain stream rises from 6.2 to 6.9 TB/s with it)
@@ -116,11 +127,13 @@ struct Step {
   int s0, s1;  // its first and one-past-last unit in the page stream
   int pg;      // first logical page
   int phys0, phys1;
+  bool first;  // first step of this piece: the query rows come with it
   bool last;   // last step of this piece of sequence b
 };
 
 template <bool REL>
 struct StepBuf {
+  u32x4 q[4];     // query fragments (first step of a piece only)
   u32x4 k[2][4];  // [tile][load]: tokens 16 t + 4 i + (lane >> 4)
   u32x4 v[2][4];
   // raw bf16 bias bits of this lane's 8 scores, [4t + i] for token
@@ -128,14 +141,31 @@ struct StepBuf {
   uint32_t rel[REL ? 8 : 1];
 };
 
-// Issue the loads of one 32-token step: 16 K/V buffer loads and, with a
-// relative bias, the 8 bias values this lane's scores need.
+// Issue the loads of one 32-token step: the query fragments (from an
+// empty resource, i.e. no memory traffic, unless the step starts a piece:
+// a piece's query then never has to be waited for apart from its step),
+// 16 K/V buffer loads and, with a relative bias, the 8 bias values this
+// lane's scores need.
 template <bool REL>
 __device__ __forceinline__ void issue_step(StepBuf<REL>& buf,
                                            const DecodeArgs& a,
                                            const Step& st, int lane_off,
                                            int page_bytes, int hq, bool head_ok,
                                            int g) {
+  {
+    const bool want = st.first && st.b >= 0;
+    const char* base = reinterpret_cast<const char*>(a.q) +
+                       (want ? (int64_t)st.b * a.HQ * kD * 2 : 0);
+    __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(base), (short)0, want ? a.HQ * kD * 2 : 0,
+        0x00020000);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+      buf.q[kk] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     rq, head_ok ? (hq * kD + 32 * kk + 8 * g) * 2 : 0x7ffffff0,
+                     0, 0));
+  }
   if constexpr (REL) {
     // rel row of sequence b: [HQ, E] bf16; out-of-band distances (and
     // padded heads) get an out-of-range offset, which reads as 0
@@ -176,8 +206,11 @@ __device__ __forceinline__ void issue_step(StepBuf<REL>& buf,
   }
 }
 
-template <int REP, bool REL>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(REL ? 1 : 2, 2)))
+// DEPTH: steps whose loads are in flight or being consumed; DEPTH - 1 steps
+// (16 KB each per wave) stream in while one is computed. One work-group per
+// CU (one wave per SIMD, the whole register file per wave).
+template <int REP, bool REL, int DEPTH>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void decode_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) char smem[];
   const int lane = threadIdx.x & 63;
@@ -261,10 +294,11 @@ void decode_kernel(DecodeArgs a) {
   int cur_n = as_const(a.ctx_lens)[cb];
   int seq_end = seq_start + vis_pages(cur_n, a.window);
   int cu = u0;
+  int last_b = -1;  // sequence of the previous step handed out
   auto next_step = [&](Step& st) {
     if (cu >= u1) {
       st.b = -1; st.n = 0; st.pg = 0; st.phys0 = -1; st.phys1 = -1;
-      st.s0 = 0; st.s1 = 0; st.last = false;
+      st.s0 = 0; st.s1 = 0; st.first = false; st.last = false;
       return;
     }
     while (seq_end <= cu) {
@@ -284,6 +318,8 @@ void decode_kernel(DecodeArgs a) {
     st.phys1 = cnt > 1 ? page_id(a, cb, st.pg + 1) : -1;
     cu += cnt;
     st.last = cu == piece_end;
+    st.first = cb != last_b;
+    last_b = cb;
   };
 
   const int row_elems = a.HKV * kD;
@@ -319,23 +355,14 @@ void decode_kernel(DecodeArgs a) {
   float m_run = -INFINITY;
   float l_part = 0.0f;
   bf16x8 qf[4];
-  int q_b = -1;
-
-  auto load_q = [&](int b) {
-    const __bf16* qrow = a.q + ((int64_t)b * a.HQ + (head_ok ? hq : 0)) * kD;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      u32x4 x = *reinterpret_cast<const u32x4*>(qrow + 32 * kk + 8 * g);
-      if (!head_ok) x = u32x4{0, 0, 0, 0};
-      qf[kk] = __builtin_bit_cast(bf16x8, x);
-    }
-    q_b = b;
-  };
 
   auto compute = [&](const StepBuf<REL>& buf, const Step& st) {
     const int n = st.n;
     const int lo = vis_lo(n, a.window);
-    if (st.b != q_b) load_q(st.b);
+    if (st.first) {
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) qf[kk] = __builtin_bit_cast(bf16x8, buf.q[kk]);
+    }
     // ---- stage K and V rows in LDS -----------------------------------------
     // (V rows of invalid tokens are zeroed: masked probabilities are 0 and
     // must not meet a NaN in P.V)
@@ -435,31 +462,52 @@ void decode_kernel(DecodeArgs a) {
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     const float lse_nat =
         l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : -INFINITY;
+    // Buffer stores with a per-row (wave-uniform) base: the lane offsets
+    // stay 32-bit, and padded heads / the LSE of lanes g != 0 / a missing
+    // LSE output get an out-of-range offset or an empty resource (dropped),
+    // so there is no divergent branch and no 64-bit address to keep live.
     const int s0 = st.s0, s1 = st.s1;
+    const int bad = 0x7ffffff0;
     if (s0 >= u0 && s1 <= u1) {
-      if (head_ok) {
-        __bf16* o = a.out + ((int64_t)b * a.HQ + hq) * kD;
+      const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+          reinterpret_cast<char*>(a.out + (int64_t)b * a.HQ * kD), (short)0,
+          a.HQ * kD * 2, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
+          reinterpret_cast<char*>(a.lse ? a.lse + (int64_t)b * a.HQ : nullptr),
+          (short)0, a.lse ? a.HQ * 4 : 0, 0x00020000);
 #pragma unroll
-        for (int blk = 0; blk < 8; ++blk) {
-          const uint32_t w0 =
-              pack_bf16x2(f32_to_bf16_bits(o_acc[blk][0] * inv),
-                          f32_to_bf16_bits(o_acc[blk][1] * inv));
-          const uint32_t w1 =
-              pack_bf16x2(f32_to_bf16_bits(o_acc[blk][2] * inv),
-                          f32_to_bf16_bits(o_acc[blk][3] * inv));
-          *reinterpret_cast<u32x2*>(o + 16 * blk + 4 * g) = u32x2{w0, w1};
-        }
-        if (a.lse && g == 0) a.lse[(int64_t)b * a.HQ + hq] = lse_nat;
+      for (int blk = 0; blk < 8; ++blk) {
+        const uint32_t w0 =
+            pack_bf16x2(f32_to_bf16_bits(o_acc[blk][0] * inv),
+                        f32_to_bf16_bits(o_acc[blk][1] * inv));
+        const uint32_t w1 =
+            pack_bf16x2(f32_to_bf16_bits(o_acc[blk][2] * inv),
+                        f32_to_bf16_bits(o_acc[blk][3] * inv));
+        __builtin_amdgcn_raw_buffer_store_b64(
+            u32x2{w0, w1}, ro,
+            head_ok ? (hq * kD + 16 * blk + 4 * g) * 2 : bad, 0, 0);
       }
-    } else if (head_ok) {
+      __builtin_amdgcn_raw_buffer_store_b32(
+          __builtin_bit_cast(uint32_t, lse_nat), rl,
+          head_ok && g == 0 ? hq * 4 : bad, 0, 0);
+    } else {
       // one piece of a longer sequence: slot b + wg is unique because
       // work-groups and sequences are both laid out in order
-      const int64_t slot = (int64_t)(b + wg) * a.HQ + hq;
-      float* po = a.part_o + slot * kD;
+      const int64_t slot0 = (int64_t)(b + wg) * a.HQ;
+      const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+          reinterpret_cast<char*>(a.part_o + slot0 * kD), (short)0,
+          a.HQ * kD * 4, 0x00020000);
+      const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
+          reinterpret_cast<char*>(a.part_lse + slot0), (short)0, a.HQ * 4,
+          0x00020000);
 #pragma unroll
       for (int blk = 0; blk < 8; ++blk)
-        *reinterpret_cast<f32x4*>(po + 16 * blk + 4 * g) = o_acc[blk] * inv;
-      if (g == 0) a.part_lse[slot] = lse_nat;
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, o_acc[blk] * inv), ro,
+            head_ok ? (hq * kD + 16 * blk + 4 * g) * 4 : bad, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b32(
+          __builtin_bit_cast(uint32_t, lse_nat), rl,
+          head_ok && g == 0 ? hq * 4 : bad, 0, 0);
     }
 #pragma unroll
     for (int blk = 0; blk < 8; ++blk) o_acc[blk] = f32x4{0, 0, 0, 0};
@@ -470,21 +518,26 @@ void decode_kernel(DecodeArgs a) {
   __syncthreads();  // every wave is done with the prefix table
 
   // ---- 4. software-pipelined walk: next step's loads fly during math ----
-  StepBuf<REL> A, B;
-  Step sa, sb;
-  next_step(sa);
-  issue_step<REL>(A, a, sa, lane_off, page_bytes, hq, head_ok, g);
-  while (true) {
-    next_step(sb);
-    issue_step<REL>(B, a, sb, lane_off, page_bytes, hq, head_ok, g);
-    compute(A, sa);
-    if (sa.last) finish_piece(sa);
-    if (sb.b < 0) break;
-    next_step(sa);
-    issue_step<REL>(A, a, sa, lane_off, page_bytes, hq, head_ok, g);
-    compute(B, sb);
-    if (sb.last) finish_piece(sb);
-    if (sa.b < 0) break;
+  // A ring of DEPTH step buffers: before step s is computed, the loads of
+  // step s + DEPTH - 1 go out into the buffer step s - 1 used. Steps past
+  // the range have no pages (zero-record resources: no memory traffic).
+  StepBuf<REL> buf[DEPTH];
+  Step stp[DEPTH];
+#pragma unroll
+  for (int k = 0; k < DEPTH - 1; ++k) {
+    next_step(stp[k]);
+    issue_step<REL>(buf[k], a, stp[k], lane_off, page_bytes, hq, head_ok, g);
+  }
+  for (;;) {
+#pragma unroll
+    for (int k = 0; k < DEPTH; ++k) {
+      const int f = (k + DEPTH - 1) % DEPTH;
+      next_step(stp[f]);
+      issue_step<REL>(buf[f], a, stp[f], lane_off, page_bytes, hq, head_ok, g);
+      if (stp[k].b < 0) return;
+      compute(buf[k], stp[k]);
+      if (stp[k].last) finish_piece(stp[k]);
+    }
   }
 }
 
@@ -561,9 +614,12 @@ int device_cus() {
 
 int waves_per_wg(int HKV) { return HKV % 4 == 0 ? 4 : (HKV % 2 == 0 ? 2 : 1); }
 
+// Three work-groups per four CUs (one wave per SIMD where they run):
+// measured on MI355X, C2 / C3 decode stream fastest between 0.75 and 0.85
+// work-groups per CU, 3-8 % ahead of one per CU and 10-20 % ahead of two.
 int default_wgs(int HKV) {
   const int ny = HKV / waves_per_wg(HKV);
-  const int g = 2 * device_cus() / ny;
+  const int g = 3 * device_cus() / (4 * ny);
   return g > 0 ? g : 1;
 }
 
@@ -581,11 +637,11 @@ template <int REP>
 void launch(const DecodeArgs& a, int G, int nw, size_t lds, hipStream_t st) {
   dim3 grid(G, a.HKV / nw);
   if (a.rel)
-    hipLaunchKernelGGL((decode_kernel<REP, true>), grid, dim3(64 * nw), lds,
-                       st, a);
+    hipLaunchKernelGGL((decode_kernel<REP, true, kDeep>), grid, dim3(64 * nw),
+                       lds, st, a);
   else
-    hipLaunchKernelGGL((decode_kernel<REP, false>), grid, dim3(64 * nw), lds,
-                       st, a);
+    hipLaunchKernelGGL((decode_kernel<REP, false, kDeep>), grid,
+                       dim3(64 * nw), lds, st, a);
 }
 
 }  // namespace

@@ -14,21 +14,23 @@
 //  * GQA grouping. A work-group owns (run, KV head, block of 256/REP
 //    queries) for all REP query heads of that KV head, i.e. 256 score rows:
 //    every K/V tile staged in LDS is used by REP heads. Each of the 8 waves
-//    owns one 32-row MFMA block (one head x 32 queries); about 200
-//    registers per wave leave room for two waves per SIMD, so one wave's
-//    MFMAs overlap the other's softmax.
+//    owns one 32-row MFMA block (one head x 32 queries), two waves per SIMD.
 //  * Transposed scores. S^T = K.Q^T (v_mfma_f32_32x32x16_bf16, keys on M,
 //    queries on N) leaves one query per lane, so the running max needs one
-//    cross-lane step (xor 32) and the running sum stays lane-local; P^T is
-//    then already the B operand of O^T = V^T.P^T, and the rescale factor of
-//    every O^T element a lane holds is that lane's own.
-//  * K tiles are stored row-major in LDS (272-byte rows: conflict-free
-//    16-byte fragment reads); V tiles are stored transposed, each thread
-//    packing 2 keys of one dimension into one 4-byte write, with the keys
-//    of a row permuted so that every P.V fragment is one 16-byte read, and
-//    the 16-byte chunks XOR-swizzled by row group to spread the writes over
-//    the banks. Tiles are double-buffered: the next tile's global loads fly
-//    while the current tile's MFMAs run; one barrier per tile.
+//    cross-lane step (a lane-half swap) and the running sum stays
+//    lane-local; P^T is then already the B operand of O^T = V^T.P^T, and
+//    the rescale factor of every O^T element a lane holds is that lane's own.
+//  * K and V tiles (64 keys) go from global memory straight into LDS
+//    (buffer_load ... lds, 1 KB per instruction, no registers), row-major
+//    with 256-byte rows and XOR swizzles chosen for the 64 LDS banks of
+//    gfx950: K 16-byte chunks by row & 15, V 64-byte blocks by row & 3. K
+//    fragments are single 16-byte reads, V^T fragments two transposed
+//    reads (ds_read_b64_tr_b16); none of them conflict. Four LDS stages,
+//    tiles issued three ahead.
+//  * Ping-pong: waves 0-3 and 4-7 alternate, half a tile apart, between an
+//    MFMA phase (P.V of a tile and the next tile's scores) and a softmax
+//    phase, so that each SIMD has one wave on the matrix core and one on
+//    the vector ALU most of the time.
 //  * Tiles wholly outside the causal/window band are never visited; only
 //    tiles that straddle the diagonal, the window start or the run end pay
 //    for per-element masking.
@@ -54,6 +56,7 @@ constexpr int kStage = 2 * kTileB;        // K tile then V tile
 constexpr int kNStage = 4;                // 128 KB of LDS per work-group
 constexpr int kPage = 16;                 // paged source: tokens per page
 constexpr float kLazy = 8.0f;             // lazy-rescale threshold (log2)
+constexpr int kRing = 5;                  // MFMA-phase fragment ring
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
@@ -433,125 +436,92 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
       }
   };
 
-  // The softmax of a tile is done in two halves so that neither MFMA phase
-  // runs alone: half 1 (max, reference point, probability pairs 0..7) runs
-  // under the previous tile's P.V MFMAs, half 2 (pairs 8..15) under the
-  // next tile's score MFMAs, about five VALU instructions per MFMA in
-  // both phases.
-  struct Soft {
-    float alpha, m_use, psum;
-    bool move;
-    uint32_t pw[16];
+  // ---- two wave groups in ping-pong ---------------------------------------
+  // Waves 0-3 and 4-7 (one of each per SIMD) alternate between an MFMA
+  // phase (P.V of tile t and the scores of tile t+1: 32 MFMAs, fragment
+  // reads, hardly any VALU) and a softmax phase (the online softmax of those
+  // scores: VALU only), half a tile apart: while one wave of a SIMD keeps
+  // the matrix core busy the other one uses the vector ALU. A work-group
+  // barrier ends every phase (two per tile); group 1 runs one phase behind
+  // group 0 (its first softmax shares the slot of group 0's first
+  // multiply), and both pass the same barriers in the same order.
+  const int grp_id = w >> 2;
+  auto full_tile = [&](int kt) {
+    return (kt + kBN - 1 <= pos_lo) && (kt + kBN <= nk) &&
+           (a.window == 0 || pos_hi - kt < a.window) && (qn == BQ);
   };
-  auto tile_max = [&](const f32x16 (&s)[2]) {
+  f32x16 sc[2];        // scores of the tile after the one being multiplied
+  bf16x8 pf[2][2];     // probabilities of the tile being multiplied
+
+  // softmax of scores `s` of the tile at kt (masking when needed): P^T
+  // fragments, running max / sum update, O^T rescale when the max moved
+  auto softmax_phase = [&](f32x16 (&s)[2], int kt, bool first) {
+    if (REL || !full_tile(kt)) mask_bias(s, kt);
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int j = 0; j < 16; j += 2)
         mx = fmaxf(fmaxf(mx, s[kb][j]), s[kb][j + 1]);
-    return mx;
-  };
-  // half 1 without interleave (masked / biased tiles, the first tile)
-  auto half1_plain = [&](const f32x16 (&s)[2], Soft& sf) {
-    sf.alpha = new_max(tile_max(s), sf.move, sf.m_use);
-    sf.psum = 0.0f;
+    bool move;
+    float m_use;
+    const float alpha = new_max(mx, move, m_use);
+    float psum = 0.0f;
+    uint32_t pw[16];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) sf.pw[q] = prob_pair(s, q, sf.m_use, sf.psum);
-  };
-  auto half2_plain = [&](const f32x16 (&s)[2], Soft& sf) {
+    for (int q = 0; q < 16; ++q) pw[q] = prob_pair(s, q, m_use, psum);
+    pack_p(pw, pf);
+    l_part = l_part * alpha + psum;
+    // O^T holds the tiles before this one: rescale it to the new reference
+    if (!first && __builtin_amdgcn_ballot_w64(move)) {
 #pragma unroll
-    for (int q = 8; q < 16; ++q) sf.pw[q] = prob_pair(s, q, sf.m_use, sf.psum);
-  };
-
-  // Phase A of tile it: the next tile's scores (16 MFMAs, K fragments read
-  // three chunks ahead) with half 2 of this tile's softmax between them,
-  // chunk by chunk. A scheduling fence after every chunk keeps the
-  // interleave, and each chunk's results are pinned in place by an empty
-  // asm that takes them as operands (pure arithmetic would otherwise be
-  // sunk to its first use, past the fences, before scheduling starts).
-  auto front = [&](int st_n, const f32x16 (&cur)[2], f32x16 (&nxt)[2],
-                   Soft& sf) {
-    const uint32_t kb0 = ka0 + lds0 + st_n * kStage;
-    auto kfrag = [&](int n) {
-      return lds_ld128((kb0 ^ (32u * (n >> 1))) + 32 * (n & 1) * kRowB);
-    };
-    bf16x8 kf[4];
-    kf[0] = kfrag(0);
-    kf[1] = kfrag(1);
-    kf[2] = kfrag(2);
-#pragma unroll
-    for (int n = 0; n < 16; ++n) {
-      if (n + 3 < 16) kf[(n + 3) & 3] = kfrag(n + 3);
-      const int kb = n & 1, kk = n >> 1;
-      nxt[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-          kf[n & 3], qf[kk], n < 2 ? f32x16{} : nxt[kb], 0, 0, 0);
-      if (n & 1) {
-        const int q = 8 + (n >> 1);
-        sf.pw[q] = prob_pair(cur, q, sf.m_use, sf.psum);
-        asm volatile("" : "+v"(sf.pw[q]), "+v"(sf.psum));
-      }
-      __builtin_amdgcn_sched_barrier(0);
+      for (int db = 0; db < 4; ++db) o_acc[db] = o_acc[db] * alpha;
     }
   };
 
-  // Phase B of tile it: O^T += V^T.P^T (16 MFMAs, V^T fragments read three
-  // ahead, the four accumulators in turn) with half 1 of the next tile's
-  // softmax between them: the max over chunks 0..3, the reference point in
-  // chunk 4, pairs 0..7 over chunks 5..15.
-  auto back = [&](int stage, const bf16x8 (&pf)[2][2],
-                  const f32x16 (&nxt)[2], Soft& sn, bool with_next) {
-    const uint32_t vb = va0 + lds0 + stage * kStage + kTileB;
+  // MFMA phase of tile t: O^T += V^T.P^T for tile t (four accumulators in
+  // turn) interleaved with the scores of tile t+1 (two accumulators), the
+  // V^T and K fragments read two MFMAs ahead
+  auto mfma_phase = [&](int t, bool with_s) {
+    const uint32_t vb = va0 + lds0 + (t & 3) * kStage + kTileB;
+    const uint32_t kb0 = ka0 + lds0 + ((t + 1) & 3) * kStage;
     auto vf_n = [&](int n) {
       const int db = n & 3, kb = n >> 3, kk = (n >> 2) & 1;
       return vfrag(vb ^ (64u * db), kb, kk);
     };
-    bf16x8 vf[4];
-    vf[0] = vf_n(0);
-    vf[1] = vf_n(1);
-    vf[2] = vf_n(2);
-    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    auto kf_n = [&](int n) {
+      return lds_ld128((kb0 ^ (32u * (n >> 1))) + 32 * (n & 1) * kRowB);
+    };
+    constexpr int R = kRing;     // fragments read R - 1 MFMAs ahead
+    bf16x8 vf[R], kf[R];
+#pragma unroll
+    for (int i = 0; i < R - 1; ++i) {
+      vf[i] = vf_n(i);
+      if (with_s) kf[i] = kf_n(i);
+    }
 #pragma unroll
     for (int n = 0; n < 16; ++n) {
-      if (n + 3 < 16) vf[(n + 3) & 3] = vf_n(n + 3);
+      if (n + R - 1 < 16) vf[(n + R - 1) % R] = vf_n(n + R - 1);
+      if (with_s && n + R - 1 < 16) kf[(n + R - 1) % R] = kf_n(n + R - 1);
       const int db = n & 3, kb = n >> 3, kk = (n >> 2) & 1;
       o_acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-          vf[n & 3], pf[kb][kk], o_acc[db], 0, 0, 0);
-      if (with_next) {
-        if (n < 4) {
-          const int kb2 = n >> 1, j0 = 8 * (n & 1);
-#pragma unroll
-          for (int j = 0; j < 8; j += 2)
-            mx[n] = fmaxf(fmaxf(mx[n], nxt[kb2][j0 + j]), nxt[kb2][j0 + j + 1]);
-          asm volatile("" : "+v"(mx[n]));
-        } else if (n == 4) {
-          sn.alpha = new_max(fmaxf(fmaxf(mx[0], mx[1]), fmaxf(mx[2], mx[3])),
-                             sn.move, sn.m_use);
-          sn.psum = 0.0f;
-          asm volatile("" : "+v"(sn.alpha), "+v"(sn.m_use));
-        } else {
-#pragma unroll
-          for (int q = 0; q < 8; ++q)
-            if (5 + (q * 11) / 8 == n) {
-              sn.pw[q] = prob_pair(nxt, q, sn.m_use, sn.psum);
-              asm volatile("" : "+v"(sn.pw[q]), "+v"(sn.psum));
-            }
-        }
+          vf[n % R], pf[kb][kk], o_acc[db], 0, 0, 0);
+      if (with_s) {
+        const int skb = n & 1, skk = n >> 1;
+        sc[skb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            kf[n % R], qf[skk], n < 2 ? f32x16{} : sc[skb], 0, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  auto full_tile = [&](int kt) {
-    return (kt + kBN - 1 <= pos_lo) && (kt + kBN <= nk) &&
-           (a.window == 0 || pos_hi - kt < a.window) && (qn == BQ);
-  };
-
-  // ---- pipeline: 4 LDS stages, tiles issued two ahead ---------------------
-  // At the top of step `it`, tiles it and it+1 are in LDS (published by a
-  // barrier) and tile it+2 is in flight; step it issues tile it+3 into the
-  // stage tile it-1 used, and before its closing barrier waits for tile
-  // it+2 (every wave issues 4 instructions per tile).
+  // ---- pipeline: 4 LDS stages, tiles issued three ahead -------------------
+  // Slot 2t: group 0 multiplies tile t, group 1 does the softmax of tile t;
+  // slot 2t+1: group 0 the softmax of tile t+1, group 1 multiplies tile t.
+  // Tile t+3 goes out at the start of slot 2t into the stage of tile t-1
+  // (last read in slot 2t-1) and must be in LDS before slot 2t+4; each
+  // wave waits for its own part at the end of every odd slot, before the
+  // barrier that publishes it (4 instructions per wave per tile).
   issue_tile(0, 0);
   if (ntiles > 1) issue_tile(1, 1);
   if (ntiles > 2) {
@@ -561,53 +531,34 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     wait_vm<0>();
   }
   __syncthreads();
-
-  int st_cur = 0;   // stage of tile it
-  Soft sf;          // softmax state of tile it (half 1 done)
-  auto step = [&](int it, f32x16 (&cur)[2], f32x16 (&nxt)[2]) {
-    const int kt = k_lo + it * kBN;
-    const int st_nxt = (st_cur + 1) & 3;
-    const bool has_next = it + 1 < ntiles;
-    // phase A: rescale O^T if some lane's reference point moved, then the
-    // next tile's scores under half 2 of this tile's softmax
-    if (__builtin_amdgcn_ballot_w64(sf.move)) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db) o_acc[db] = o_acc[db] * sf.alpha;
-    }
-    if (!REL && has_next) {
-      front(st_nxt, cur, nxt, sf);
-    } else {
-      half2_plain(cur, sf);
-      if (has_next) scores(st_nxt, nxt);
-    }
-    bf16x8 pf[2][2];
-    pack_p(sf.pw, pf);
-    l_part = l_part * sf.alpha + sf.psum;
-    // phase B: P.V of this tile under half 1 of the next tile's softmax
-    const bool more = it + 3 < ntiles;
-    if (more) issue_tile(it + 3, (st_cur + 3) & 3);
-    if (has_next && !REL && full_tile(kt + kBN)) {
-      back(st_cur, pf, nxt, sf, true);
-    } else {
-      back(st_cur, pf, nxt, sf, false);
-      if (has_next) {
-        mask_bias(nxt, kt + kBN);
-        half1_plain(nxt, sf);
-      }
-    }
-    if (more) wait_vm<4>(); else wait_vm<0>();
+  auto odd_end = [&](int t) {
+    if (t + 3 < ntiles) wait_vm<4>(); else wait_vm<0>();
     __syncthreads();
-    st_cur = st_nxt;
   };
-
-  f32x16 sa[2], sb[2];
-  scores(0, sa);
-  if (REL || !full_tile(k_lo)) mask_bias(sa, k_lo);
-  half1_plain(sa, sf);
-  for (int it = 0; it < ntiles; ++it) {
-    step(it, sa, sb);
-    sa[0] = sb[0];
-    sa[1] = sb[1];
+  if (grp_id == 0) {
+    scores(0, sc);
+    softmax_phase(sc, k_lo, true);
+    for (int t = 0; t < ntiles; ++t) {
+      if (t + 3 < ntiles) issue_tile(t + 3, (t + 3) & 3);
+      const bool has_next = t + 1 < ntiles;
+      mfma_phase(t, has_next);
+      __syncthreads();
+      if (has_next) softmax_phase(sc, k_lo + (t + 1) * kBN, false);
+      odd_end(t);
+    }
+  } else {
+    for (int t = 0; t < ntiles; ++t) {
+      if (t + 3 < ntiles) issue_tile(t + 3, (t + 3) & 3);
+      if (t == 0) {
+        scores(0, sc);
+        softmax_phase(sc, k_lo, true);
+      } else {
+        softmax_phase(sc, k_lo + t * kBN, false);
+      }
+      __syncthreads();
+      mfma_phase(t, t + 1 < ntiles);
+      odd_end(t);
+    }
   }
 
   // ---- finalise: l over both lane halves, normalise, store --------------

@@ -108,7 +108,7 @@ int tmopt_kv_write_paged(const void* k, const void* v, int64_t k_stride_tok,
 
 /*
  * Work-groups tmopt_attn_decode_paged launches when num_workgroups == 0
- * (two per compute unit of the current device, divided among the
+ * (three per four compute units of the current device, divided among the
  * HKV / 4 head groups).
  */
 int tmopt_attn_decode_default_workgroups(int HKV);

@@ -126,10 +126,17 @@ class DecodeStepGraph:
 class MixedStepGraph:
     """Config-5 step: for every layer, append the step's tokens (chunked
     prefill runs + one token per decode row) through the layer's block
-    table, run the paged chunked prefill, then the paged decode. All three
-    kernels per layer are captured into ONE hipGraph for the whole step."""
+    table, then run the paged chunked prefill and the paged decode. All
+    three kernels per layer are captured into ONE hipGraph for the whole
+    step.
 
-    def __init__(self, step, min_pages=8, num_workgroups=0):
+    With overlap=True the decode of a layer runs on a second stream, forked
+    after the append and joined before the next layer: the HBM-bound decode
+    and the MFMA-bound prefill then share the GPU instead of taking turns
+    (in the graph they are two independent nodes between the append and
+    the next layer)."""
+
+    def __init__(self, step, min_pages=8, num_workgroups=0, overlap=True):
         self.s = step
         dev = step.q_decode.device
         B, HQ, D = step.q_decode.shape
@@ -141,6 +148,8 @@ class MixedStepGraph:
         self.lse_d = torch.empty((B, HQ), dtype=torch.float32, device=dev)
         self.ws = attn.decode_workspace(B, HQ, HKV, dev, num_workgroups)
         self.min_pages, self.num_workgroups = min_pages, num_workgroups
+        self.overlap = overlap
+        self.side = torch.cuda.Stream(device=dev) if overlap else None
         self.graph = StepGraph(self.run_eager, dev)
 
     def layer(self, l, parts=("kv", "prefill", "decode")):
@@ -167,8 +176,22 @@ class MixedStepGraph:
                               workspace=self.ws)
 
     def run_eager(self):
+        if not self.overlap:
+            for l in range(self.s.n_layers):
+                self.layer(l)
+            return
+        main = torch.cuda.current_stream()
         for l in range(self.s.n_layers):
-            self.layer(l)
+            self.layer(l, ("kv",))
+            fork = torch.cuda.Event()
+            fork.record(main)
+            self.side.wait_event(fork)
+            with torch.cuda.stream(self.side):
+                self.layer(l, ("decode",))
+            self.layer(l, ("prefill",))
+            join = torch.cuda.Event()
+            join.record(self.side)
+            main.wait_event(join)
 
     def capture(self):
         self.graph.capture()

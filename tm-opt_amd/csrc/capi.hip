@@ -1,4 +1,5 @@
-// Library-wide C-ABI plumbing: thread-local error text and version string.
+// Library-wide C-ABI plumbing: thread-local error text, version string and
+// the compute-unit count of the current device.
 #include <stdarg.h>
 #include <stdio.h>
 
@@ -24,6 +25,20 @@ int check_launch(const char* what) {
     return TMOPT_ELAUNCH;
   }
   return TMOPT_OK;
+}
+
+int device_cus() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount,
+                              dev) != hipSuccess || n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
 }
 
 }  // namespace tmopt

@@ -86,6 +86,11 @@ __device__ __forceinline__ void lds_st128(uint32_t addr, u32x4 v) {
   *(lds_u32x4*)(uintptr_t)addr = v;
 }
 
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
+__device__ __forceinline__ void lds_st64(uint32_t addr, u32x2 v) {
+  *(lds_u32x2*)(uintptr_t)addr = v;
+}
+
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
 // i % 4 of the 8-byte chunks addressed by lanes 4j + i / 4 (j = 0..3), i.e.
 // a 4 x 16 block of 16-bit values comes back transposed
@@ -104,6 +109,8 @@ __device__ __forceinline__ void wave_lds_sync() {
 void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
 void clear_error();
 int check_launch(const char* what);
+// compute units of the current device (cached per device; 256 if unknown)
+int device_cus();
 
 }  // namespace tmopt
 

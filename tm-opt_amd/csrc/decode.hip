@@ -594,24 +594,6 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
                    : -INFINITY;
 }
 
-struct DeviceInfo {
-  int cus = 0;
-};
-
-int device_cus() {
-  static DeviceInfo info[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (info[dev].cus == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount,
-                              dev) != hipSuccess || n <= 0)
-      n = 256;
-    info[dev].cus = n;
-  }
-  return info[dev].cus;
-}
-
 int waves_per_wg(int HKV) { return HKV % 4 == 0 ? 4 : (HKV % 2 == 0 ? 2 : 1); }
 
 // Three work-groups per four CUs (one wave per SIMD where they run):

@@ -568,8 +568,16 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // ---- finalise: l over both lane halves, normalise, store --------------
   const float l_tot = l_part + __shfl_xor(l_part, 32);
   const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (!qok) return;
-  __bf16* orow = a.out + (int64_t)(t0 + qi) * a.o_st + (int64_t)head * a.o_sh;
+  if (a.lse && h2 == 0 && qok)
+    a.lse[(int64_t)head * as_const(a.cu)[a.S] + t0 + qi] =
+        l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : -INFINITY;
+  // O^T goes through LDS (free after the last barrier) so that the global
+  // stores are whole rows: the wave writes its 32 x 128 block query-major
+  // (256-byte rows, 16-byte chunks swizzled by row & 15, so neither the
+  // 8-byte writes nor the 16-byte reads conflict), then each store
+  // instruction covers 4 complete rows (16 lanes x 16 bytes per row)
+  // instead of 16 bytes of 32 rows.
+  const uint32_t ob = lds0 + (uint32_t)w * (32 * kRowB);
 #pragma unroll
   for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -578,12 +586,31 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
                                       f32_to_bf16_bits(o_acc[db][4 * g4 + 1] * inv));
       const uint32_t w1 = pack_bf16x2(f32_to_bf16_bits(o_acc[db][4 * g4 + 2] * inv),
                                       f32_to_bf16_bits(o_acc[db][4 * g4 + 3] * inv));
-      *reinterpret_cast<u32x2*>(orow + 32 * db + 8 * g4 + 4 * h2) =
-          u32x2{w0, w1};
+      const int c = 4 * db + g4;    // 16-byte chunk: dims 8c .. 8c+7
+      lds_st64(ob + l32 * kRowB + 16 * (c ^ (l32 & 15)) + 8 * h2,
+               u32x2{w0, w1});
     }
-  if (a.lse && h2 == 0)
-    a.lse[(int64_t)head * as_const(a.cu)[a.S] + t0 + qi] =
-        l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : -INFINITY;
+  wave_lds_sync();
+  const int qrow0 = q0 + 32 * (w % QSUB);   // query of the block's row 0
+  const int c16 = lane & 15;
+  const bool al16 = ((a.o_st | a.o_sh) & 7) == 0 &&
+                    ((uintptr_t)a.out & 15) == 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 4 * i + (lane >> 4);
+    const u32x4 x = __builtin_bit_cast(
+        u32x4, lds_ld128(ob + r * kRowB + 16 * (c16 ^ (r & 15))));
+    if (qrow0 + r < len) {
+      __bf16* const dst = a.out + (int64_t)(t0 + qrow0 + r) * a.o_st +
+                          (int64_t)head * a.o_sh + 8 * c16;
+      if (al16) {
+        *reinterpret_cast<u32x4*>(dst) = x;
+      } else {
+        reinterpret_cast<u32x2*>(dst)[0] = u32x2{x[0], x[1]};
+        reinterpret_cast<u32x2*>(dst)[1] = u32x2{x[2], x[3]};
+      }
+    }
+  }
 }
 
 template <int REP>

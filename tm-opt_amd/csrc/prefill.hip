@@ -237,17 +237,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   const int qpos = prior + qi;
 
   // ---- Q fragments: B operand of S^T (column = query, k = dims) --------
-  bf16x8 qf[8];
-  {
-    const __bf16* row = a.q + (int64_t)(t0 + (qok ? qi : 0)) * a.q_st +
-                        (int64_t)head * a.q_sh;
-#pragma unroll
-    for (int kk = 0; kk < 8; ++kk) {
-      u32x4 x = *reinterpret_cast<const u32x4*>(row + 16 * kk + 8 * h2);
-      if (!qok) x = u32x4{0, 0, 0, 0};
-      qf[kk] = __builtin_bit_cast(bf16x8, x);
-    }
-  }
+  bf16x8 qf[8];   // loaded through LDS in the prologue below
 
   // ---- tile loads: global -> LDS directly (buffer_load ... lds) ----------
   // Wave w moves key rows 4w..4w+3 and 32+4w..32+4w+3 of the K and the V
@@ -526,15 +516,38 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // (last read in slot 2t-1) and must be in LDS before slot 2t+4; each
   // wave waits for its own part at the end of every odd slot, before the
   // barrier that publishes it (4 instructions per wave per tile).
+  // The queries come first, by the same direct loads: the wave's 32 rows
+  // (1 KB = 4 rows per instruction, 16-byte chunks swizzled by row & 15)
+  // into stages 2 and 3, which hold no tile until tile 2 goes out after
+  // every wave has its fragments; rows past the run end arrive as zeros.
+  const uint32_t qlds = lds0 + 2 * kStage + (uint32_t)w * (32 * kRowB);
+  {
+    const int qrow0 = q0 + 32 * (w % QSUB);
+    const int64_t qspan = ((int64_t)(len - qrow0 - 1) * a.q_st + kD) * 2;
+    const i32x4 rq = make_rsrc(
+        a.q + (int64_t)(t0 + qrow0) * a.q_st + (int64_t)head * a.q_sh,
+        qrow0 < len ? (uint32_t)qspan : 0u);
+    const int qst_b = (int)(a.q_st * 2);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 4 * i + grp;
+      dma_b128(rq, qlds + i * 1024, r * qst_b + 16 * (slot ^ (r & 15)));
+    }
+  }
   issue_tile(0, 0);
   if (ntiles > 1) issue_tile(1, 1);
-  if (ntiles > 2) {
-    issue_tile(2, 2);
-    wait_vm<4>();
-  } else {
-    wait_vm<0>();
+  wait_vm<0>();
+  __syncthreads();
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    u32x4 x = __builtin_bit_cast(
+        u32x4,
+        lds_ld128(qlds + l32 * kRowB + 16 * ((2 * kk + h2) ^ (l32 & 15))));
+    if (!qok) x = u32x4{0, 0, 0, 0};
+    qf[kk] = __builtin_bit_cast(bf16x8, x);
   }
   __syncthreads();
+  if (ntiles > 2) issue_tile(2, 2);
   auto odd_end = [&](int t) {
     if (t + 3 < ntiles) wait_vm<4>(); else wait_vm<0>();
     __syncthreads();
@@ -706,6 +719,9 @@ extern "C" int tmopt_attn_prefill_varlen(
                   TMOPT_EINVAL,
                   "prefill: k/v rows must be 16-byte aligned (strides %% 8)");
   }
+  TMOPT_REQUIRE(((int64_t)max_seqlen_q * q_stride_tok + kD) * 2 < (1ll << 31),
+                TMOPT_EUNSUPPORTED,
+                "prefill: a run's q span must stay below 2 GiB");
   TMOPT_REQUIRE(q_stride_tok % 8 == 0 && q_stride_head % 8 == 0 &&
                     o_stride_tok % 4 == 0 && o_stride_head % 4 == 0 &&
                     (uintptr_t)q % 16 == 0 && (uintptr_t)out % 8 == 0,

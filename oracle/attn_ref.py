@@ -78,7 +78,8 @@ def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
 
 
 def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, prior_lens=None,
-                   k_pool=None, v_pool=None, block_table=None, q_block=256):
+                   k_pool=None, v_pool=None, block_table=None, q_block=256,
+                   rel=None):
     """Causal (optionally windowed) attention over packed runs.
 
     Follows _attn_prefill_kernel (engine/pyengine/kernels/attn_prefill.py:
@@ -89,6 +90,9 @@ def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, prior_lens=None,
     GQA head h reads KV head h // REP. Prior keys (and, when block_table is
     given, all keys) come from the paged pools through the table; otherwise
     the run's own keys are the packed k/v rows.
+    rel (optional, [total, HQ, E]): query row t of head h adds
+    rel[t, h, qpos - kpos] to the scaled score inside 0 <= qpos - kpos < E
+    and nothing outside (attn_prefill.py:114-120, rel_bias model.py:137-158).
 
     Returns (out [total, HQ, D] fp32, lse [HQ, total] fp32)."""
     total, HQ, D = q.shape
@@ -128,6 +132,13 @@ def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, prior_lens=None,
             qb = q[t0 + j0:t0 + j1].float().permute(1, 0, 2)    # [HQ, m, D]
             s = torch.matmul(qb, Kh[:, k_lo:k_hi].transpose(1, 2)) * scale
             d = qp[:, None] - kp[None, :]
+            if rel is not None:
+                E = rel.shape[2]
+                r = rel[t0 + j0:t0 + j1].float().permute(1, 0, 2)  # [HQ,m,E]
+                band = (d >= 0) & (d < E)
+                idx = d.clamp(0, E - 1)[None].expand(HQ, -1, -1)
+                s = s + torch.where(band[None], torch.gather(r, 2, idx),
+                                    torch.zeros(()))
             keep = d >= 0
             if window:
                 keep &= d < window

@@ -3,9 +3,10 @@
 Tolerances (BASELINE): outputs max-abs 2e-2 / rtol 1e-2, LSE 1e-3.
 Covers ragged lengths around the 32-query / 64-key tile edges, causal and
 windowed masks, GQA 4 and 8, strided inputs, chunked prefill reading prior
-context from a shuffled paged cache, the q = 0 closed form
-(LSE = ln(#visible keys)), determinism, and config 4 at full size checked on
-sampled query rows.
+context from a shuffled paged cache, the fused relative bias (band shorter
+than the runs, so most key tiles carry none; packed and paged sources), the
+q = 0 closed form (LSE = ln(#visible keys)), determinism, and config 4 at
+full size checked on sampled query rows.
 """
 import math
 
@@ -181,3 +182,61 @@ def test_config4_sampled_rows(tm, dev, window):
             assert_out_close(out[t0 + j], ref_o, f"C4 w={window} seq{i} q{j}")
             assert_lse_close(lse[:, t0 + j], ref_l,
                              f"C4 w={window} seq{i} q{j}")
+
+
+@pytest.mark.parametrize("E,window", [(95, 0), (1, 0), (80, 256), (300, 64)])
+@pytest.mark.parametrize("hq,hkv", [(32, 4), (64, 16)])
+def test_bias_band_shorter_than_runs(tm, dev, E, window, hq, hkv):
+    """Fused bias rel[t, h, dist] inside 0 <= dist < E: with E well below
+    the run lengths most key tiles lie wholly outside the band and skip the
+    bias, so one item mixes tiles with and without it; odd E and query
+    positions of both parities exercise the realigned bias loads."""
+    g = torch.Generator().manual_seed(31)
+    case = _wl().make_prefill("bias", 23, lens=[700, 333, 65, 1],
+                              window=window, hq=hq, hkv=hkv)
+    total = case.q.shape[0]
+    rel = (torch.randn((total, hq, E), generator=g) * 2.0).to(torch.bfloat16)
+    ref_o, ref_l = attn_ref.prefill_varlen(case.q, case.k, case.v,
+                                           case.cu_seqlens, case.scale,
+                                           window=window, rel=rel)
+    out, lse = _gpu(tm, case, dev, rel=rel.to(dev))
+    assert_out_close(out, ref_o, f"bias E={E} w={window} {hq}/{hkv}")
+    assert_lse_close(lse, ref_l, f"bias E={E} w={window} {hq}/{hkv}")
+
+
+def test_bias_paged_prior_context(tm, dev):
+    """Fused bias on the paged source with prior context: dist counts from
+    the query's position (prior + j), so the band reaches into the prior
+    keys."""
+    g = torch.Generator().manual_seed(19)
+    wl = _wl()
+    prior = [0, 40, 300, 5]
+    lens = [150, 64, 97, 1]
+    S, HQ, HKV, D, E = len(lens), 32, 4, 128, 70
+    table, P = wl.paged_layout(lens, g, pool_factor=2, prior=prior)
+    tot = [p + t for p, t in zip(prior, lens)]
+    kp = torch.full((P, 16, HKV, D), float("nan"), dtype=torch.bfloat16)
+    vp = torch.full((P, 16, HKV, D), float("nan"), dtype=torch.bfloat16)
+    for i in range(S):
+        pos = torch.arange(tot[i])
+        pages = table[i][pos // 16].long()
+        kp[pages, pos % 16] = torch.randn((tot[i], HKV, D),
+                                          generator=g).to(torch.bfloat16)
+        vp[pages, pos % 16] = torch.randn((tot[i], HKV, D),
+                                          generator=g).to(torch.bfloat16)
+    cu = torch.zeros(S + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens), 0)
+    q = torch.randn((int(cu[-1]), HQ, D), generator=g).to(torch.bfloat16)
+    rel = torch.randn((int(cu[-1]), HQ, E), generator=g).to(torch.bfloat16)
+    pr = torch.tensor(prior, dtype=torch.int32)
+    ref_o, ref_l = attn_ref.prefill_varlen(q, None, None, cu, 0.08,
+                                           prior_lens=pr, k_pool=kp,
+                                           v_pool=vp, block_table=table,
+                                           rel=rel)
+    out, lse = tm.prefill_varlen(q.to(dev), None, None, cu.to(dev), 0.08,
+                                 prior_lens=pr.to(dev), k_pool=kp.to(dev),
+                                 v_pool=vp.to(dev), block_table=table.to(dev),
+                                 rel=rel.to(dev))
+    torch.cuda.synchronize()
+    assert_out_close(out, ref_o, "paged bias")
+    assert_lse_close(lse, ref_l, "paged bias")

@@ -374,3 +374,24 @@ def test_prefill_semantics_bias_closed_form():
             max=E - 1)]), torch.ones(()))
         want = (w[:, None] * vb[:t + 1]).sum(0) / w.sum()
         assert torch.allclose(out[0, t, 0], want, atol=1e-5)
+
+
+def test_varlen_bias_matches_padded_semantics():
+    """The packed oracle's fused bias (rel [total, HQ, E]) against the
+    padded-batch restatement of the model semantics, which gathers the
+    bias independently (torch.gather over [B, H, T, E]): E shorter than the
+    runs, with and without a window."""
+    g = torch.Generator().manual_seed(43)
+    B, H, HK, T, D, E = 2, 4, 2, 45, 16, 11
+    q = torch.randn((B, H, T, D), generator=g).to(torch.bfloat16)
+    k = torch.randn((B, HK, T, D), generator=g).to(torch.bfloat16)
+    v = torch.randn((B, HK, T, D), generator=g).to(torch.bfloat16)
+    rel = torch.randn((B, H, T, E), generator=g).to(torch.bfloat16)
+    cu = torch.tensor([0, T, 2 * T])
+    pk = lambda x: x.transpose(1, 2).reshape(B * T, x.shape[1], x.shape[3])
+    for window in (None, 7, 30):
+        a = attn_ref.prefill_reference_semantics(q, k, v, rel,
+                                                 torch.arange(T), window)
+        b, _ = attn_ref.prefill_varlen(pk(q), pk(k), pk(v), cu, 1.0 / D,
+                                       window=window or 0, rel=pk(rel))
+        assert (a.reshape(B * T, H, D) - b).abs().max() < 1e-5, window

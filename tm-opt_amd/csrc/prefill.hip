@@ -346,23 +346,80 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
   };
 
-  // per-element mask (causal, window, run end) and optional fused bias
-  auto mask_bias = [&](f32x16 (&s)[2], int kt) {
+  // Fused bias rows of this wave's 32 queries: one buffer resource from
+  // the first query's row (lane offsets: row l32, 32-bit), covering the
+  // rows of the run only, so reads past them return zeros.
+  // (The resource starts at the dword holding that row's first value and
+  // ends at the dword holding the last row's last value, so that the dword
+  // loads below are aligned whatever the strides and every dword holding a
+  // value of the rows is in range.)
+  const int rel_row0 = q0 + 32 * (w % QSUB);
+  const int rel_nrow = REL ? min(32, len - rel_row0) : 0;
+  const char* const rel_first =
+      REL ? reinterpret_cast<const char*>(a.rel + (int64_t)(t0 + rel_row0) *
+                                                      a.r_st +
+                                          (int64_t)head * a.r_sh)
+          : nullptr;
+  const int rel_mis = (int)((uintptr_t)rel_first & 3);   // 0 or 2
+  [[maybe_unused]] const __amdgpu_buffer_rsrc_t rrel =
+      __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<char*>(rel_first - rel_mis), (short)0,
+          rel_nrow > 0 ? ((int)(((int64_t)(rel_nrow - 1) * a.r_st +
+                                 a.rel_extent) * 2) + rel_mis + 3) & ~3
+                       : 0,
+          0x00020000);
+  [[maybe_unused]] const int rrow_b =
+      REL ? rel_mis + l32 * (int)(a.r_st * 2) : 0;
+
+  // per-element mask (causal, window, run end) and, on tiles within the
+  // bias band, the fused bias
+  auto mask_bias = [&](f32x16 (&s)[2], int kt, bool with_bias) {
     if constexpr (REL) {
-      // the scores move to the log2 domain: s*scale*log2e + rel*log2e,
-      // rel gathered at rel[q, h, dist] for 0 <= dist < E, zero outside
-      const __bf16* rrow = a.rel + (int64_t)(t0 + (qok ? qi : 0)) * a.r_st +
-                           (int64_t)head * a.r_sh;
+      if (with_bias) {
+        // the scores move to the log2 domain: s*scale*log2e + rel*log2e,
+        // rel[q, h, dist] for 0 <= dist < E, zero outside. The lane's keys
+        // come in runs of four (key0 .. key0+3, dist d0 .. d0-3), whose
+        // four bf16 values are adjacent in the row: the three dwords from
+        // the one holding rel[d0-3], realigned by 0 or 2 bytes. One load
+        // per dword: a dword holding a value of the rows is in range, and
+        // its load cannot be voided by a neighbour that is not.
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+        for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int kp = kt + 32 * kb + 8 * (j >> 2) + 4 * h2 + (j & 3);
-          const int dist = qpos - kp;
-          const bool band = qok && dist >= 0 && dist < a.rel_extent;
-          const float bias = band ? (float)rrow[dist] : 0.0f;
-          s[kb][j] = __builtin_fmaf(s[kb][j], a.scale_log2, bias * kLog2e);
-        }
+          for (int g = 0; g < 4; ++g) {
+            const int key0 = kt + 32 * kb + 8 * g + 4 * h2;
+            const int d0 = qpos - key0;
+            const int b = rrow_b + 2 * (d0 - 3);
+            // A dword before the first row (only masked keys use it) gets
+            // an offset past the range. The whole offset goes in the lane
+            // register: the range check does not see a constant part the
+            // compiler might move into the instruction, so b4 = -4 with
+            // +4 there would void a dword that is in range.
+            auto rel_dword = [&](int off) {
+              off = off < 0 ? 0x7ffffff0 : off;
+              asm volatile("" : "+v"(off));
+              return __builtin_amdgcn_raw_buffer_load_b32(rrel, off, 0, 0);
+            };
+            const int b4 = b & ~3;
+            const uint32_t x0 = rel_dword(b4);
+            const uint32_t x1 = rel_dword(b4 + 4);
+            const uint32_t x2 = rel_dword(b4 + 8);
+            const uint32_t sh = (uint32_t)(b & 3);
+            const uint32_t w0 = __builtin_amdgcn_alignbyte(x1, x0, sh);
+            const uint32_t w1 = __builtin_amdgcn_alignbyte(x2, x1, sh);
+            // element 4g + i is key0 + i, dist d0 - i
+            const uint32_t hv[4] = {w1 & 0xffff0000u, w1 << 16,
+                                    w0 & 0xffff0000u, w0 << 16};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int dist = d0 - i;
+              const bool band = qok && dist >= 0 && dist < a.rel_extent;
+              const float bias = band ? __builtin_bit_cast(float, hv[i]) : 0.0f;
+              s[kb][4 * g + i] =
+                  __builtin_fmaf(s[kb][4 * g + i], a.scale_log2, bias * kLog2e);
+            }
+          }
+      }
     }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -384,13 +441,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   float l_part = 0.0f;
   // Without a bias the max runs on the raw scores (scale > 0 commutes with
   // max) and each probability is one fma + exp2: p = 2^(s*scale*log2e - m).
-  const float sl2 = REL ? 1.0f : a.scale_log2;
+  // (on tiles that carry the fused bias the scores are already in that
+  // domain, and the factor is 1)
 
   // Lazy rescaling: the running max (log2 domain) only moves when the
   // tile's max exceeds it by more than kLazy, so probabilities stay below
   // 2^kLazy and O^T / l are rescaled on few tiles; O / l and the LSE are
   // exact for any reference point.
-  auto new_max = [&](float mx, bool& move, float& m_use) {
+  auto new_max = [&](float mx, float sl2, bool& move, float& m_use) {
     const auto sw = __builtin_amdgcn_permlane32_swap(
         __builtin_bit_cast(uint32_t, mx), __builtin_bit_cast(uint32_t, mx),
         false, false);
@@ -405,7 +463,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     return alpha;
   };
   // probability pair q (kb = q >> 3, kk = (q >> 2) & 1, e = q & 3)
-  auto prob_pair = [&](const f32x16 (&s)[2], int q, float m_use,
+  auto prob_pair = [&](const f32x16 (&s)[2], int q, float sl2, float m_use,
                        float& psum) {
     const int kb = q >> 3, kk = (q >> 2) & 1, e = q & 3;
     const float p0 =
@@ -446,7 +504,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // softmax of scores `s` of the tile at kt (masking when needed): P^T
   // fragments, running max / sum update, O^T rescale when the max moved
   auto softmax_phase = [&](f32x16 (&s)[2], int kt, bool first) {
-    if (REL || !full_tile(kt)) mask_bias(s, kt);
+    // the bias band: some pair of the tile has dist = q - k < E (the
+    // smallest dist is pos_lo - (kt + 63))
+    const bool with_bias = REL && pos_lo - (kt + kBN - 1) < a.rel_extent;
+    if (with_bias || !full_tile(kt)) mask_bias(s, kt, with_bias);
+    const float sl2 = with_bias ? 1.0f : a.scale_log2;
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -455,11 +517,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         mx = fmaxf(fmaxf(mx, s[kb][j]), s[kb][j + 1]);
     bool move;
     float m_use;
-    const float alpha = new_max(mx, move, m_use);
+    const float alpha = new_max(mx, sl2, move, m_use);
     float psum = 0.0f;
     uint32_t pw[16];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) pw[q] = prob_pair(s, q, m_use, psum);
+    for (int q = 0; q < 16; ++q) pw[q] = prob_pair(s, q, sl2, m_use, psum);
     pack_p(pw, pf);
     l_part = l_part * alpha + psum;
     // O^T holds the tiles before this one: rescale it to the new reference
@@ -686,6 +748,14 @@ extern "C" int tmopt_attn_prefill_varlen(
   TMOPT_REQUIRE(scale > 0.0f, TMOPT_EINVAL, "prefill: scale must be > 0");
   TMOPT_REQUIRE(rel == nullptr || rel_extent > 0, TMOPT_EINVAL,
                 "prefill: rel_extent=%d", rel_extent);
+  TMOPT_REQUIRE(rel == nullptr ||
+                    (rel_stride_tok >= rel_extent && rel_stride_head >= 0 &&
+                     (64 * rel_stride_tok + 2 * (int64_t)rel_extent) <
+                         (1ll << 31)),
+                TMOPT_EUNSUPPORTED,
+                "prefill: rel rows must not overlap, and 32 rows must span "
+                "less than 2 GiB (stride_tok=%lld, extent=%d)",
+                (long long)rel_stride_tok, rel_extent);
   {
     const int bq = 256 / rep;
     const int64_t blocks =

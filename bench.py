@@ -8,8 +8,10 @@ hd128, ctx U[1024, 8192], shuffled pool): one step = one decode-attention
 call over the whole batch, inputs resident in HBM. Two pool sets rotate so
 that consecutive steps never re-read the same bytes from the 256 MB
 Infinity Cache. value = algorithmic bytes of the K timed steps / their wall
-time; roofline.achieved = algorithmic bytes per launch / the launch's mean
-duration from HIP events on the launch stream.
+time; roofline.achieved = algorithmic bytes per launch / the mean launch
+duration from the two HIP events that bracket the K timed launches on the
+launch stream (no event between launches: recording one there adds ~7 us
+to a ~100 us decode step).
 
 Secondary lines in "extra": config 3 (window-4096 decode), config 4 (varlen
 prefill, global and window 4096) and the KV-cache write, each with its own
@@ -41,22 +43,23 @@ def _metric():
 
 
 def time_launches(fn, sets, steps, warmup):
-    """Warm up, then time exactly `steps` launches (rotating input sets):
-    returns (wall seconds for the timed steps, list of per-launch ms from
-    HIP events recorded on the launch stream)."""
+    """Warm up, then time exactly `steps` launches (rotating input sets),
+    synchronised on both sides: returns (wall seconds for the timed steps,
+    mean ms per launch from the two HIP events on the launch stream that
+    bracket them)."""
     for i in range(warmup):
         fn(sets[i % len(sets)])
     torch.cuda.synchronize()
-    ev = [(torch.cuda.Event(enable_timing=True),
-           torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    e0.record()
     for i in range(steps):
-        ev[i][0].record()
         fn(sets[i % len(sets)])
-        ev[i][1].record()
+    e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    return wall, [a.elapsed_time(b) for a, b in ev]
+    return wall, e0.elapsed_time(e1) / steps
 
 
 def bench_decode(tm, wl, make, steps, warmup, n_sets=2, min_pages=8,
@@ -80,9 +83,8 @@ def bench_decode(tm, wl, make, steps, warmup, n_sets=2, min_pages=8,
                         num_workgroups=num_workgroups, out=out, lse=lse,
                         workspace=w)
 
-    wall, per = time_launches(fn, sets, steps, warmup)
+    wall, mean_ms = time_launches(fn, sets, steps, warmup)
     nbytes = c0.algorithmic_bytes()
-    mean_ms = sum(per) / len(per)
     return {
         "workload": c0.name, "B": c0.B, "window": c0.window,
         "bytes_per_launch": nbytes, "ms_per_step": wall * 1e3 / steps,
@@ -112,9 +114,8 @@ def bench_prefill(tm, wl, window, steps, warmup, n_sets=2):
                           window=c.window, max_seqlen=max_len, out=out,
                           lse=lse)
 
-    wall, per = time_launches(fn, sets, steps, warmup)
+    wall, mean_ms = time_launches(fn, sets, steps, warmup)
     flops = c0.algorithmic_flops()
-    mean_ms = sum(per) / len(per)
     return {
         "workload": c0.name, "lens": c0.lens, "window": window,
         "flops_per_launch": flops, "ms_per_step": wall * 1e3 / steps,
@@ -241,7 +242,10 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # ~10 ms of decode steps: the first configuration of a fresh process
+    # otherwise times the GPU's clock ramp (C2 measured 108 us per step
+    # after 10 warm-up steps, 98 us once warm)
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--min-pages", type=int, default=8)
     ap.add_argument("--wgs", type=int, default=0)

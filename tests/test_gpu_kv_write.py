@@ -164,3 +164,45 @@ def test_t_b3_ring_pin(tm, dev):
         got = kv_ref.gather(kv_ref.as_u16(vp), [6, 2], 13, page=4,
                             table_wrap=2, lo=5)
         assert np.array_equal(got, kv_ref.as_u16(vs[5:]))
+
+
+@pytest.mark.parametrize("wrap", [0, 9])
+def test_write_paged_long_runs_and_single_tokens(tm, dev, wrap):
+    """A mixed step: two long runs beside a hundred one-token rows, so the
+    launch packs several 16-byte chunks per lane (a grid sized by the
+    longest run would otherwise be mostly empty work-groups)."""
+    g = torch.Generator().manual_seed(29 + wrap)
+    H, D = 4, 128
+    lens = [2000] + [1] * 100 + [777]
+    S = len(lens)
+    start = torch.randint(0, 300, (S,), generator=g).tolist()
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    k = _bf16((T, H, D), g)
+    v = _bf16((T, H, D), g)
+    # every row gets distinct pages for the positions it writes; the rest
+    # of its table row points outside the pool
+    per = [wrap if wrap else (s + n + 15) // 16 for s, n in zip(start, lens)]
+    width = max(per)
+    P = sum(per) + 8
+    perm = torch.randperm(P, generator=g).to(torch.int32)
+    table = torch.full((S, width), P + 5, dtype=torch.int32)
+    off = 0
+    for i, n in enumerate(per):
+        table[i, :n] = perm[off:off + n]
+        off += n
+    table[3, start[3] // 16 % (wrap or 10**9)] = P + 11   # skipped write
+    kp = _bf16((P, 16, H, D), g)
+    vp = _bf16((P, 16, H, D), g)
+    want_k = kv_ref.write_paged(kv_ref.as_u16(kp).copy(), kv_ref.as_u16(k),
+                                cu, start, table.numpy(), 16, wrap)
+    want_v = kv_ref.write_paged(kv_ref.as_u16(vp).copy(), kv_ref.as_u16(v),
+                                cu, start, table.numpy(), 16, wrap)
+    kd, vd = kp.to(dev), vp.to(dev)
+    tm.kv_write_paged(k.to(dev), v.to(dev), table.to(dev),
+                      torch.tensor(start, dtype=torch.int32, device=dev), kd,
+                      vd, cu_seqlens=torch.from_numpy(cu).to(dev),
+                      table_wrap=wrap)
+    torch.cuda.synchronize()
+    assert np.array_equal(kv_ref.as_u16(kd), want_k)
+    assert np.array_equal(kv_ref.as_u16(vd), want_v)

@@ -2,9 +2,11 @@
 //
 // Replaces the reference's torch index_put_ appends
 // (engine/pyengine/model.py:938-948 decode, engine/pyengine/kv.py:89-103 and
-// :193-205 prefill). Pure byte movement: every lane moves one 16-byte chunk
-// of K and the same chunk of V, so one wave covers 1 KB of a token row and
-// global reads and writes are fully coalesced. HBM-bound; bit-exact.
+// :193-205 prefill). Pure byte movement: a lane moves 16-byte chunks of K
+// and the same chunks of V (consecutive lanes, consecutive chunks of a
+// token row), so global reads and writes are fully coalesced. Bit-exact.
+// Index math is 32-bit: the 64-bit divisions of a first version cost more
+// than the copy.
 #include "common.h"
 
 namespace tmopt {
@@ -30,8 +32,16 @@ __global__ __launch_bounds__(256) void kv_write_slots_kernel(
   vp[dst] = v[t * v_st + h * v_sh + c];
 }
 
-// grid = (ceil(max_seqlen * per_tok / 256), num_seqs). Token positions and
-// pages are derived in-kernel from cu_seqlens/start_pos/block_table.
+// grid = (ceil(max_seqlen * per_tok / (256 R)), num_seqs): work-group x of
+// sequence seq covers chunks [256 R x, 256 R (x+1)) of that sequence's
+// tokens (chunk = 16 bytes of one (token, kv-head) row), lane i the chunks
+// 256 R x + 256 p + i, p < R. Token positions and pages are derived
+// in-kernel from cu_seqlens/start_pos/block_table. The grid is sized by the
+// longest run, so R > 1 keeps a call with a few long runs and many one-token
+// rows (a mixed prefill + decode step) from dispatching tens of thousands of
+// empty work-groups; every load of a work-group (table entries, K and V) is
+// issued before its first store.
+template <int R>
 __global__ __launch_bounds__(256) void kv_write_paged_kernel(
     const u32x4* __restrict__ k, const u32x4* __restrict__ v, int64_t k_st,
     int64_t k_sh, int64_t v_st, int64_t v_sh,
@@ -42,34 +52,53 @@ __global__ __launch_bounds__(256) void kv_write_paged_kernel(
     u32x4* __restrict__ vp, int64_t num_pages) {
   const int seq = blockIdx.y;
   const int per_tok = HKV * D16;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t tl = gid / per_tok;
-  int64_t t0 = seq, len = 1;
+  int t0 = seq, len = 1;
   if (cu_seqlens != nullptr) {
     t0 = cu_seqlens[seq];
-    len = (int64_t)cu_seqlens[seq + 1] - t0;
+    len = cu_seqlens[seq + 1] - t0;
   }
-  if (tl >= len) return;
-  const int64_t pos = (int64_t)start_pos[seq] + tl;
-  if (pos < 0) return;
+  // 32-bit index math (the host keeps max_seqlen * per_tok below 2^31;
+  // positions are int32)
+  const int base = blockIdx.x * (256 * R);
+  if (base >= len * per_tok) return;
+  const int p0 = start_pos[seq];
   // Ring pools keep only the last table_wrap*page_size positions: a token
   // that a later token of this same call overwrites is dropped, so the
   // parallel scatter has no write-write race (kv.py:97-98).
-  if (table_wrap > 0 &&
-      pos < (int64_t)start_pos[seq] + len - (int64_t)table_wrap * page_size)
-    return;
-  int64_t lp = pos / page_size;
-  if (table_wrap > 0) lp %= table_wrap;
-  const int64_t page = block_table[(int64_t)seq * bt_stride + lp];
-  if (page < 0 || page >= num_pages) return;
-  const int64_t row = page * page_size + pos % page_size;
-  const int rem = (int)(gid - tl * per_tok);
-  const int h = rem / D16;
-  const int c = rem - h * D16;
-  const int64_t t = t0 + tl;
-  const int64_t dst = (row * HKV + h) * D16 + c;
-  kp[dst] = k[t * k_st + h * k_sh + c];
-  vp[dst] = v[t * v_st + h * v_sh + c];
+  const int keep_from = table_wrap > 0 ? p0 + len - table_wrap * page_size : 0;
+  const int32_t* trow = block_table + (int64_t)seq * bt_stride;
+  int page[R], off[R];
+  u32x4 kx[R], vx[R];
+  // branch-free, and nothing waits for a load before every load of the
+  // work-group is out: a chunk that writes nothing reads from a valid
+  // dummy address (the run's first row, table entry 0) and gets off = -1;
+  // off = the chunk's offset inside its page row set, page = table entry
+#pragma unroll
+  for (int p = 0; p < R; ++p) {
+    const int gid = base + 256 * p + (int)threadIdx.x;
+    const int tl = gid / per_tok;
+    const int pos = p0 + tl;
+    const bool live = tl < len && pos >= 0 && pos >= keep_from;
+    int lp = live ? pos / page_size : 0;
+    if (table_wrap > 0) lp %= table_wrap;
+    page[p] = trow[lp];
+    const int rem = live ? gid - tl * per_tok : 0;
+    const int h = rem / D16;
+    const int c = rem - h * D16;
+    const int64_t t = t0 + (live ? tl : 0);
+    kx[p] = k[t * k_st + h * k_sh + c];
+    vx[p] = v[t * v_st + h * v_sh + c];
+    off[p] = live ? ((pos % page_size) * HKV + h) * D16 + c : -1;
+  }
+  asm volatile("" ::: "memory");   // every load above goes out first
+  const int64_t page_chunks = (int64_t)page_size * HKV * D16;
+#pragma unroll
+  for (int p = 0; p < R; ++p) {
+    if (off[p] < 0 || page[p] < 0 || page[p] >= num_pages) continue;
+    const int64_t dst = (int64_t)page[p] * page_chunks + off[p];
+    kp[dst] = kx[p];
+    vp[dst] = vx[p];
+  }
 }
 
 int check_kv_common(const void* k, const void* v, int64_t k_st, int64_t k_sh,
@@ -152,14 +181,37 @@ extern "C" int tmopt_kv_write_paged(
   if (st) return st;
   const int D16 = D / 8;
   const int64_t work = (int64_t)max_seqlen * HKV * D16;
-  const int64_t bx = (work + 255) / 256;
-  TMOPT_REQUIRE(bx < (1ll << 31), TMOPT_EINVAL,
-                "kv_write_paged: max_seqlen too large");
-  hipLaunchKernelGGL(kv_write_paged_kernel, dim3((unsigned)bx, num_seqs),
-                     dim3(256), 0, (hipStream_t)stream, (const u32x4*)k,
-                     (const u32x4*)v, k_stride_tok / 8, k_stride_head / 8,
-                     v_stride_tok / 8, v_stride_head / 8, cu_seqlens,
-                     start_pos, block_table, bt_stride, table_wrap, page_size,
-                     HKV, D16, (u32x4*)k_pool, (u32x4*)v_pool, num_pages);
+  // chunks per lane: the smallest power of two (up to 16) that keeps the
+  // grid within 32768 work-groups. Measured on config 5's append (2 runs of
+  // 2048 tokens + 96 one-token rows, graph replays): 1 chunk per lane (50K
+  // work-groups, mostly empty) 13.4 us, 2: 9.0 us, 4: 11.0 us, 16: 37 us
+  // (too few busy work-groups for the long runs)
+  int R = 1;
+  for (;;) {
+    const int64_t bx_r = (work + 256 * R - 1) / (256 * R);
+    if (R == 16 || bx_r == 1 || bx_r * num_seqs <= 32768) break;
+    R *= 2;
+  }
+  const int64_t bx = (work + 256 * R - 1) / (256 * R);
+  TMOPT_REQUIRE(work + 256 * R < (1ll << 31), TMOPT_EINVAL,
+                "kv_write_paged: max_seqlen * HKV * D / 8 must stay below "
+                "2^31");
+  const dim3 grid((unsigned)bx, num_seqs);
+  hipStream_t hs = (hipStream_t)stream;
+#define TMOPT_KVW(RR)                                                        \
+  hipLaunchKernelGGL(kv_write_paged_kernel<RR>, grid, dim3(256), 0, hs,       \
+                     (const u32x4*)k, (const u32x4*)v, k_stride_tok / 8,     \
+                     k_stride_head / 8, v_stride_tok / 8, v_stride_head / 8, \
+                     cu_seqlens, start_pos, block_table, bt_stride,          \
+                     table_wrap, page_size, HKV, D16, (u32x4*)k_pool,        \
+                     (u32x4*)v_pool, num_pages)
+  switch (R) {
+    case 1: TMOPT_KVW(1); break;
+    case 2: TMOPT_KVW(2); break;
+    case 4: TMOPT_KVW(4); break;
+    case 8: TMOPT_KVW(8); break;
+    default: TMOPT_KVW(16); break;
+  }
+#undef TMOPT_KVW
   return check_launch("kv_write_paged");
 }

@@ -18,11 +18,12 @@ __global__ __launch_bounds__(256) void kv_write_slots_kernel(
     int64_t k_sh, int64_t v_st, int64_t v_sh,
     const int64_t* __restrict__ slots, int64_t T, int HKV, int D16,
     u32x4* __restrict__ kp, u32x4* __restrict__ vp, int64_t pool_rows) {
-  const int64_t per_tok = (int64_t)HKV * D16;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t t = gid / per_tok;
+  // 32-bit index math (the host keeps T * HKV * D16 below 2^31)
+  const int per_tok = HKV * D16;
+  const int gid = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  const int t = gid / per_tok;
   if (t >= T) return;
-  const int rem = (int)(gid - t * per_tok);
+  const int rem = gid - t * per_tok;
   const int h = rem / D16;
   const int c = rem - h * D16;
   const int64_t row = slots[t];
@@ -143,7 +144,8 @@ extern "C" int tmopt_kv_write_slots(const void* k, const void* v,
   const int D16 = D / 8;
   const int64_t work = T * HKV * D16;
   const int64_t blocks = (work + 255) / 256;
-  TMOPT_REQUIRE(blocks < (1ll << 31), TMOPT_EINVAL, "kv_write_slots: T too large");
+  TMOPT_REQUIRE(work + 256 < (1ll << 31), TMOPT_EINVAL,
+                "kv_write_slots: T * HKV * D / 8 must stay below 2^31");
   hipLaunchKernelGGL(kv_write_slots_kernel, dim3((unsigned)blocks), dim3(256),
                      0, (hipStream_t)stream, (const u32x4*)k, (const u32x4*)v,
                      k_stride_tok / 8, k_stride_head / 8, v_stride_tok / 8,

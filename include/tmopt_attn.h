@@ -70,6 +70,7 @@ const char* tmopt_version(void);
  * k_pool,v_pool: [pool_rows, HKV, D] contiguous.
  * Bit-exact copy. Duplicate rows in one call are written in unspecified
  * order (the same contract as index_put_ without accumulate).
+ * T * HKV * D / 8 must stay below 2^31 (TMOPT_EINVAL otherwise).
  */
 int tmopt_kv_write_slots(const void* k, const void* v, int64_t k_stride_tok,
                          int64_t k_stride_head, int64_t v_stride_tok,
@@ -90,7 +91,9 @@ int tmopt_kv_write_slots(const void* k, const void* v, int64_t k_stride_tok,
  * table_wrap > 0 a token that a later token of the same call would
  * overwrite is dropped, as RingKV.append does (kv.py:97-98).
  * cu_seqlens may be NULL: then sequence i has exactly one token, k row i
- * (the decode step). max_seqlen bounds the per-sequence token count.
+ * (the decode step). max_seqlen bounds the per-sequence token count, and
+ * max_seqlen * HKV * D / 8 must stay below 2^31 (TMOPT_EINVAL otherwise);
+ * positions are int32.
  * Table entries outside [0, num_pages) are skipped, never dereferenced.
  */
 int tmopt_kv_write_paged(const void* k, const void* v, int64_t k_stride_tok,
@@ -200,7 +203,11 @@ int tmopt_attn_decode_paged(const void* q, const void* k_pool,
  * rel, rel_extent: optional fused relative bias (NULL = off): row r of q
  *         (token) and head h own rel[r * rel_stride_tok + h * rel_stride_head
  *         + dist] for 0 <= dist = pos_q - pos_k < rel_extent; pairs outside
- *         that band get 0 (attn_prefill.py:115-120).
+ *         that band get 0 (attn_prefill.py:115-120). Rows must not overlap
+ *         (rel_stride_tok >= rel_extent) and 32 rows must span less than
+ *         2 GiB, else TMOPT_EUNSUPPORTED.
+ * A run's q rows (and, on the packed source, its k / v rows) must span less
+ * than 2 GiB (max_seqlen_q * stride): TMOPT_EUNSUPPORTED otherwise.
  * max_seqlen_q bounds every len_i (it sizes the grid).
  * out:    [total_q, HQ, D] with element strides (o_stride_tok,
  *         o_stride_head), D contiguous.

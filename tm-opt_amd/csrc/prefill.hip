@@ -380,9 +380,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         // rel[q, h, dist] for 0 <= dist < E, zero outside. The lane's keys
         // come in runs of four (key0 .. key0+3, dist d0 .. d0-3), whose
         // four bf16 values are adjacent in the row: the three dwords from
-        // the one holding rel[d0-3], realigned by 0 or 2 bytes. One load
-        // per dword: a dword holding a value of the rows is in range, and
-        // its load cannot be voided by a neighbour that is not.
+        // the one holding rel[d0-3], realigned by 0 or 2 bytes.
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -390,20 +388,35 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
             const int key0 = kt + 32 * kb + 8 * g + 4 * h2;
             const int d0 = qpos - key0;
             const int b = rrow_b + 2 * (d0 - 3);
-            // A dword before the first row (only masked keys use it) gets
-            // an offset past the range. The whole offset goes in the lane
-            // register: the range check does not see a constant part the
-            // compiler might move into the instruction, so b4 = -4 with
-            // +4 there would void a dword that is in range.
-            auto rel_dword = [&](int off) {
-              off = off < 0 ? 0x7ffffff0 : off;
-              asm volatile("" : "+v"(off));
-              return __builtin_amdgcn_raw_buffer_load_b32(rrel, off, 0, 0);
-            };
+            // One 16-byte load from the dword holding rel[d0-3]: the range
+            // check is per dword (a dword past the range reads 0, the ones
+            // before it are returned), and the resource ends at a dword
+            // boundary, so every value of the rows arrives. The whole
+            // offset goes in the lane register, where the check sees it.
+            // Offsets before the first row occur only on the wave's first
+            // row near dist 0; then the wave takes three dword loads, one
+            // with an offset past the range for each dword before the row.
             const int b4 = b & ~3;
-            const uint32_t x0 = rel_dword(b4);
-            const uint32_t x1 = rel_dword(b4 + 4);
-            const uint32_t x2 = rel_dword(b4 + 8);
+            uint32_t x0, x1, x2;
+            if (!__builtin_amdgcn_ballot_w64(b4 < 0)) {
+              int off = b4;
+              asm volatile("" : "+v"(off));
+              const u32x4 x = __builtin_bit_cast(
+                  u32x4, __builtin_amdgcn_raw_buffer_load_b128(rrel, off, 0,
+                                                               0));
+              x0 = x[0];
+              x1 = x[1];
+              x2 = x[2];
+            } else {
+              auto rel_dword = [&](int off) {
+                off = off < 0 ? 0x7ffffff0 : off;
+                asm volatile("" : "+v"(off));
+                return __builtin_amdgcn_raw_buffer_load_b32(rrel, off, 0, 0);
+              };
+              x0 = rel_dword(b4);
+              x1 = rel_dword(b4 + 4);
+              x2 = rel_dword(b4 + 8);
+            }
             const uint32_t sh = (uint32_t)(b & 3);
             const uint32_t w0 = __builtin_amdgcn_alignbyte(x1, x0, sh);
             const uint32_t w1 = __builtin_amdgcn_alignbyte(x2, x1, sh);

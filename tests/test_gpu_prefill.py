@@ -94,6 +94,25 @@ def test_strided_inputs(tm, dev):
     assert torch.all(outw[:, :8] == 0) and torch.all(outw[:, 40:] == 0)
 
 
+def test_output_rows_8_byte_aligned(tm, dev):
+    """Output head rows 132 elements apart (8-byte but not 16-byte
+    aligned): the row-wise store falls back to 8-byte stores, and the 4
+    padding elements after every row stay untouched."""
+    case = _wl().make_prefill("o8", 24, lens=[45, 130, 1])
+    T, HQ, D = case.q.shape
+    ref_o, ref_l = attn_ref.prefill_varlen(case.q, case.k, case.v,
+                                           case.cu_seqlens, case.scale)
+    outw = torch.full((T, HQ, D + 4), 7.0, dtype=torch.bfloat16, device=dev)
+    out, lse = tm.prefill_varlen(case.q.to(dev), case.k.to(dev),
+                                 case.v.to(dev), case.cu_seqlens.to(dev),
+                                 case.scale, out=outw[:, :, :D])
+    torch.cuda.synchronize()
+    assert outw[:, :, :D].stride(1) % 8 == 4
+    assert_out_close(outw[:, :, :D].cpu(), ref_o, "8-byte rows")
+    assert_lse_close(lse.cpu(), ref_l, "8-byte rows")
+    assert torch.all(outw[:, :, D:] == 7.0)
+
+
 @pytest.mark.parametrize("window", [0, 48])
 def test_paged_prior_context(tm, dev, window):
     """Chunked prefill: each run's keys = prior context + its own tokens,

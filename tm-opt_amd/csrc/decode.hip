@@ -544,7 +544,8 @@ void decode_kernel(DecodeArgs a) {
 // Merge the pieces of every sequence that several work-groups shared:
 // grid (B, ceil(HQ / 8)), 8 heads x 32 lanes per work-group, 4 dims per
 // lane; pieces are merged in work-group order (deterministic, no atomics),
-// four pieces' loads in flight at a time.
+// eight pieces' loads in flight at a time (one round for the pieces of most
+// sequences: the load latency, not the bytes, is what this kernel waits on).
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
   const int b = blockIdx.x;
   const int C = as_const(a.geo)[0];
@@ -560,18 +561,19 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a) {
   const int64_t slot0 = (int64_t)(b + wfirst) * a.HQ + h;
   float m = -INFINITY, sum = 0.0f;
   f32x4 acc = f32x4{0, 0, 0, 0};
-  for (int k = 0; k < np; k += 4) {
-    float l4[4];
-    f32x4 o4[4];
+  constexpr int kBatch = 8;
+  for (int k = 0; k < np; k += kBatch) {
+    float l4[kBatch];
+    f32x4 o4[kBatch];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kBatch; ++j) {
       const bool in = k + j < np;
       const int64_t slot = slot0 + (int64_t)(in ? k + j : 0) * a.HQ;
       l4[j] = in ? a.part_lse[slot] : -INFINITY;
       o4[j] = *reinterpret_cast<const f32x4*>(a.part_o + slot * kD + d0);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kBatch; ++j) {
       const float m_new = fmaxf(m, l4[j]);
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
       const float keep = fast_exp2((m - m_use) * kLog2e);

@@ -60,6 +60,22 @@ __device__ __forceinline__ float fast_log2(float x) {
   return __builtin_amdgcn_logf(x);
 }
 
+// Reductions over lane pairs (l, l ^ 16) and (l, l ^ 32) by the gfx950
+// row-swap instructions (VALU, a few cycles) instead of LDS-routed shuffles.
+// permlane16_swap(x, x) returns the rows (r0, r0, r2, r2) and (r1, r1, r3,
+// r3) (permlane32_swap likewise for the wave halves), so for every lane the
+// two results are its own value and its partner's, in some order: the
+// sum / max of the two is the pair's.
+__device__ __forceinline__ float lane_pair(float x, int dist, bool want_max) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = dist == 16
+                     ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                     : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const float a = __builtin_bit_cast(float, (uint32_t)r[0]);
+  const float b = __builtin_bit_cast(float, (uint32_t)r[1]);
+  return want_max ? fmaxf(a, b) : a + b;
+}
+
 // View of read-only global memory through the constant address space: a
 // wave-uniform load through it becomes a scalar (s_load) fetch that waits on
 // lgkmcnt, so it never drains the wave's in-flight vector loads. Only for

@@ -411,8 +411,7 @@ void decode_kernel(DecodeArgs a) {
         mx = fmaxf(mx, v);
       }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = lane_pair(lane_pair(mx, 16, true), 32, true);
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
     const float alpha = fast_exp2(m_run - m_use);
@@ -457,8 +456,7 @@ void decode_kernel(DecodeArgs a) {
   auto finish_piece = [&](const Step& st) {
     const int b = st.b;
     float l_tot = l_part;
-    l_tot += __shfl_xor(l_tot, 16);
-    l_tot += __shfl_xor(l_tot, 32);
+    l_tot = lane_pair(lane_pair(l_tot, 16, false), 32, false);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     const float lse_nat =
         l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : -INFINITY;

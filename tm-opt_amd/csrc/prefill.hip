@@ -121,10 +121,18 @@ struct PrefillArgs {
   int rel_extent;
 };
 
+// Sum over the wave, wave-uniform: within each 16-lane row by DPP (xor 1,
+// xor 2, half-row mirror, row mirror: a few cycles each), then the four row
+// sums by lane reads. (The schedule below takes ~10 of these per
+// work-group; as ds_bpermute shuffles, 6 LDS round trips each, they cost
+// microseconds of every work-group's start.)
 __device__ __forceinline__ int wave_sum(int v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // xor 1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // xor 2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // 7 - i
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);  // 15 - i
+  return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) +
+         __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
 }
 
 // query blocks of run s (lane-varying s)

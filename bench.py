@@ -3,9 +3,9 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
 
 A step is one pass of the hot path over one batch of synthetic input. The
-headline workload is BASELINE config 2 (global paged decode, B=64, 32Q/4KV,
-hd128, ctx U[1024, 8192], shuffled pool): one step = one decode-attention
-call over the whole batch, inputs resident in HBM. Two pool sets rotate so
+headline workload is config 2 of BASELINE.json (global paged decode, B=64,
+32Q/4KV, hd128, ctx U[1024, 8192], shuffled pool): one step = one
+decode-attention call over the whole batch, inputs resident in HBM. Two pool sets rotate so
 that consecutive steps never re-read the same bytes from the 256 MB
 Infinity Cache. value = algorithmic bytes of the K timed steps / their wall
 time; roofline.achieved = algorithmic bytes per launch / the mean launch

@@ -2,7 +2,7 @@
 see oracle/__init__.py; never imported by the product path).
 
 Every function computes in float32 from the bf16 inputs upcast exactly (not
-regenerated), which is the BASELINE oracle: softmax(scale * Q K^T + bias +
+regenerated), the oracle BASELINE.json asks for: softmax(scale * Q K^T + bias +
 mask) V with a natural-log LSE. The reference rounds the probabilities to
 bf16 before P.V (engine/pyengine/kernels/attn_swa.py:110-112); the oracle
 does not, and the tolerance absorbs that rounding.

@@ -1,8 +1,8 @@
 """Shared comparison helpers for the parity tests."""
 import torch
 
-# BASELINE tolerances: attention outputs max-abs 2e-2 / rtol 1e-2 against
-# the fp32 oracle, LSE within 1e-3 (absolute, natural log).
+# Tolerances from BASELINE.json: attention outputs max-abs 2e-2 / rtol
+# 1e-2 against the fp32 oracle, LSE within 1e-3 (absolute, natural log).
 OUT_ATOL = 2e-2
 OUT_RTOL = 1e-2
 LSE_ATOL = 1e-3

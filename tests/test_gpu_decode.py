@@ -1,8 +1,8 @@
 """Parity of the HIP split-KV paged decode kernel against the fp32 oracle.
 
-Tolerances (BASELINE): outputs max-abs 2e-2 / rtol 1e-2, LSE 1e-3. Pools are
-NaN-poisoned outside the pages a sequence owns, so any stray read shows up
-as a non-finite output. Geometry edges follow the reference's own arm
+Tolerances: outputs max-abs 2e-2 / rtol 1e-2, LSE 1e-3.
+Pools are NaN-poisoned outside the pages a sequence owns, so any stray read
+shows up as a non-finite output. Geometry edges follow the reference's own arm
 (engine/pyengine/tests/t_fused_attn.py:119-122): positions 0, 3, 200, 511,
 512, 513, 800, 1500 and a dead row at position 0.
 """

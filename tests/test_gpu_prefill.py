@@ -1,6 +1,6 @@
 """Parity of the HIP varlen prefill kernel against the fp32 oracle.
 
-Tolerances (BASELINE): outputs max-abs 2e-2 / rtol 1e-2, LSE 1e-3.
+Tolerances: outputs max-abs 2e-2 / rtol 1e-2, LSE 1e-3.
 Covers ragged lengths around the 32-query / 64-key tile edges, causal and
 windowed masks, GQA 4 and 8, strided inputs, chunked prefill reading prior
 context from a shuffled paged cache, the fused relative bias (band shorter

@@ -1,5 +1,5 @@
-"""Seeded synthetic inputs for the five BASELINE configurations, plus the
-algorithmic-work counters the roofline figures divide by.
+"""Seeded synthetic inputs for the five configurations of BASELINE.json,
+plus the algorithmic-work counters the roofline figures divide by.
 
 Seeds: one torch.Generator per configuration, seeded 20261201 + index
 (C1..C5 -> 1..5). Draw order: lengths, then the block-table permutation,

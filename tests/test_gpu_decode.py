@@ -161,3 +161,35 @@ def test_empty_and_zero_length(tm, dev):
                         c.ctx_lens[:0], c.scale)
     assert e[0].shape == (0, 32, 128)
     assert math.isfinite(float(lse[0].max()))
+
+
+@pytest.mark.parametrize("window", [0, 700])
+def test_rising_scores_rescale(tm, dev, window):
+    """Scores that climb with the key position, so the running max of every
+    split moves past the lazy threshold again and again and the partials
+    are merged across very different maxima: key p of a sequence is
+    s * 0.02 p + noise, the query 0.5 s + noise (s a +-1 pattern per KV
+    head); the score rises ~0.11 per key, up to ~330 at 3000 keys."""
+    from importlib import import_module
+    wl = import_module("tm-opt_amd.workloads")
+    case = wl.make_decode("rise", 12, 6, 200, 3000, window=window)
+    B, hq, D = case.q.shape
+    hkv = case.k_pool.shape[2]
+    g = torch.Generator().manual_seed(6)
+    s = torch.where(torch.rand(hkv, D, generator=g) < 0.5, -1.0, 1.0)
+    kp = case.k_pool.float()
+    for b in range(B):
+        n = int(case.ctx_lens[b])
+        lo = max(0, n - window) if window else 0
+        p = torch.arange(lo, n)
+        pages = case.block_table[b, p // 16].long()
+        kp[pages, p % 16] = s[None] * (0.02 * p.float())[:, None, None] + \
+            0.3 * torch.randn(p.numel(), hkv, D, generator=g)
+    case.k_pool.copy_(kp.to(torch.bfloat16))
+    case.q.copy_((0.5 * s.repeat_interleave(hq // hkv, 0)[None] +
+                  0.1 * torch.randn(B, hq, D, generator=g)).to(torch.bfloat16))
+    ref_o, ref_l = _oracle(case)
+    for mp, wgs in ((1, 0), (8, 5)):
+        out, lse = _run(tm, case, dev, min_pages=mp, num_workgroups=wgs)
+        assert_out_close(out, ref_o, f"rising w={window} mp={mp}")
+        assert_lse_close(lse, ref_l, f"rising w={window} mp={mp}")

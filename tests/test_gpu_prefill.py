@@ -259,3 +259,33 @@ def test_bias_paged_prior_context(tm, dev):
     torch.cuda.synchronize()
     assert_out_close(out, ref_o, "paged bias")
     assert_lse_close(lse, ref_l, "paged bias")
+
+
+@pytest.mark.parametrize("window", [0, 300])
+@pytest.mark.parametrize("hq,hkv", [(32, 4), (64, 16)])
+def test_rising_scores_rescale(tm, dev, window, hq, hkv):
+    """Scores that climb along the keys, so the running max moves past the
+    lazy threshold on every key tile and the accumulated O^T and row sum are
+    rescaled over and over (with factors that underflow to 0 for the oldest
+    terms): key t of a run is s * 0.02 t + noise, every query 0.5 s + noise
+    (s a +-1 pattern per KV head), i.e. the score rises ~0.11 per key, ~7
+    per 64-key tile, up to ~110 at the end of a 1000-token run."""
+    case = _wl().make_prefill("rise", 24, lens=[1000, 130, 65, 700],
+                              window=window, hq=hq, hkv=hkv)
+    g = torch.Generator().manual_seed(5)
+    s = torch.where(torch.rand(hkv, 128, generator=g) < 0.5, -1.0, 1.0)
+    cu = case.cu_seqlens.tolist()
+    pos = torch.cat([torch.arange(cu[i + 1] - cu[i])
+                     for i in range(len(cu) - 1)]).float()
+    k = s[None] * (0.02 * pos)[:, None, None] + \
+        0.3 * torch.randn(pos.numel(), hkv, 128, generator=g)
+    q = 0.5 * s.repeat_interleave(hq // hkv, 0)[None] + \
+        0.1 * torch.randn(pos.numel(), hq, 128, generator=g)
+    case.k.copy_(k.to(torch.bfloat16))
+    case.q.copy_(q.to(torch.bfloat16))
+    ref_o, ref_l = attn_ref.prefill_varlen(case.q, case.k, case.v,
+                                           case.cu_seqlens, case.scale,
+                                           window=window)
+    out, lse = _gpu(tm, case, dev)
+    assert_out_close(out, ref_o, f"rising w={window} {hq}/{hkv}")
+    assert_lse_close(lse, ref_l, f"rising w={window} {hq}/{hkv}")

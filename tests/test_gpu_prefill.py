@@ -289,3 +289,27 @@ def test_rising_scores_rescale(tm, dev, window, hq, hkv):
     out, lse = _gpu(tm, case, dev)
     assert_out_close(out, ref_o, f"rising w={window} {hq}/{hkv}")
     assert_lse_close(lse, ref_l, f"rising w={window} {hq}/{hkv}")
+
+
+def test_score_spike_underflows_old_terms(tm, dev):
+    """One key per run scores ~150 above the rest (a jump of ~215 in the
+    log2 domain): the running max leaps once, the rescale factor of
+    everything before underflows to 0, and later keys add terms ~e^-150
+    relative to it. Queries before the spike see ordinary scores."""
+    case = _wl().make_prefill("spike", 25, lens=[900, 300], window=0)
+    g = torch.Generator().manual_seed(7)
+    hq, hkv = case.q.shape[1], case.k.shape[1]
+    s = torch.where(torch.rand(hkv, 128, generator=g) < 0.5, -1.0, 1.0)
+    cu = case.cu_seqlens.tolist()
+    q = s.repeat_interleave(hq // hkv, 0)[None].expand(
+        case.q.shape[0], -1, -1)
+    k = case.k.float()
+    for i, at in ((0, 517), (1, 70)):
+        k[cu[i] + at] = s * 13.25      # q.k * scale = 128 * 13.25 / 11.3
+    case.q.copy_(q.to(torch.bfloat16))
+    case.k.copy_(k.to(torch.bfloat16))
+    ref_o, ref_l = attn_ref.prefill_varlen(case.q, case.k, case.v,
+                                           case.cu_seqlens, case.scale)
+    out, lse = _gpu(tm, case, dev)
+    assert_out_close(out, ref_o, "spike")
+    assert_lse_close(lse, ref_l, "spike")

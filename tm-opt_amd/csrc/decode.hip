@@ -232,12 +232,17 @@ void decode_kernel(DecodeArgs a) {
     for (int b0 = 0; b0 < a.B; b0 += blockDim.x) {
       const int b = b0 + threadIdx.x;
       const int v = b < a.B ? vis_pages(as_const(a.ctx_lens)[b], a.window) : 0;
+      // inclusive scan over the wave by DPP (VALU, no LDS round trips):
+      // within each 16-lane row by shifts of 1, 2, 4, 8, then row 0's
+      // total into row 1 and row 2's into row 3, then rows 0-1's total into
+      // rows 2-3
       int x = v;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(x, off);
-        if (lane >= off) x += y;
-      }
+      x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xF, 0xF, true);  // shr 1
+      x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xF, 0xF, true);  // shr 2
+      x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xF, 0xF, true);  // shr 4
+      x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xF, 0xF, true);  // shr 8
+      x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xA, 0xF, false); // bcast 15
+      x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xC, 0xF, false); // bcast 31
       if (lane == 63) wsum[w] = x;
       __syncthreads();
       int before = carry;

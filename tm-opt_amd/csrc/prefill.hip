@@ -56,7 +56,7 @@ constexpr int kStage = 2 * kTileB;        // K tile then V tile
 constexpr int kNStage = 4;                // 128 KB of LDS per work-group
 constexpr int kPage = 16;                 // paged source: tokens per page
 constexpr float kLazy = 8.0f;             // lazy-rescale threshold (log2)
-constexpr int kRing = 5;                  // MFMA-phase fragment ring
+constexpr int kRing = 4;                  // MFMA-phase fragment ring
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
@@ -554,7 +554,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 
   // MFMA phase of tile t: O^T += V^T.P^T for tile t (four accumulators in
   // turn) interleaved with the scores of tile t+1 (two accumulators), the
-  // V^T and K fragments read two MFMAs ahead
+  // V^T and K fragments read kRing - 1 MFMAs ahead (3: measured ~1% over 4
+  // and 5 ahead on 4K-16K runs)
   auto mfma_phase = [&](int t, bool with_s) {
     // the SIMD's issue port goes to this wave's MFMAs first; the softmax
     // wave fills the slots in between (measured ~2% over equal priority)

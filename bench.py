@@ -157,9 +157,24 @@ def bench_mixed(tm, wl, steps, warmup):
     torch.cuda.synchronize()
     step_ms = e0.elapsed_time(e1) / steps
     kinds = {}
+    # the step's decode grid is sized to share the chip with the prefill;
+    # the stand-alone grid (the library default) gives the kernel's own rate
+    B, HQ, _ = st.q_decode.shape
+    HKV = st.pool_g[0].shape[2]
+    ws_full = tm.decode_workspace(B, HQ, HKV, st.q_decode.device)
+    n_chunks = len(st.chunk_lens)
+
+    def decode_full(l):
+        kp, vp = st.pool_g if st.is_global[l] else st.pool_s
+        tm.decode_paged(st.q_decode, kp, vp, st.tables[l][n_chunks:],
+                        st.dec_ctx, st.scale,
+                        window=0 if st.is_global[l] else st.window,
+                        out=ms.out_d, lse=ms.lse_d, workspace=ws_full)
+
     for name, l in (("global", 3), ("swa", 0)):
         parts = {p: _event_ms(lambda p=p: ms.layer(l, (p,)), 3)
                  for p in ("kv", "prefill", "decode")}
+        us_full = _event_ms(lambda: decode_full(l), 3) * 1e3
         dec_b = st.decode_bytes(l)
         pf = st.prefill_flops(l)
         kinds[name] = {
@@ -167,6 +182,9 @@ def bench_mixed(tm, wl, steps, warmup):
             "us_prefill": parts["prefill"] * 1e3,
             "us_decode": parts["decode"] * 1e3,
             "decode_gbs": dec_b / (parts["decode"] * 1e-3) / 1e9,
+            "decode_workgroups": ms.num_workgroups,
+            "us_decode_standalone_grid": us_full,
+            "decode_gbs_standalone_grid": dec_b / (us_full * 1e-6) / 1e9,
             "prefill_tflops": pf / (parts["prefill"] * 1e-3) / 1e12,
             "kv_write_gbs": st.kv_write_bytes() / (parts["kv"] * 1e-3) / 1e9,
             "decode_bytes": dec_b, "prefill_flops": pf}

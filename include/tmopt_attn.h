@@ -145,6 +145,9 @@ size_t tmopt_attn_decode_workspace_size(int B, int HQ, int HKV, int D,
  *               (0 = empty: output 0, LSE -inf).
  * window:       0 = global; W > 0 = sliding window, keys k with
  *               pos - k < W only (pages wholly outside are never read).
+ *               With table_wrap > 0, 0 < window <= table_wrap * page_size
+ *               (TMOPT_EINVAL otherwise: the ring no longer holds older
+ *               keys).
  * scale:        softmax scale applied to q.k.
  * rel, rel_extent: optional fused relative bias (NULL = off): rel is
  *               [B, HQ, rel_extent] contiguous and the score of key k gets

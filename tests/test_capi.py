@@ -63,6 +63,14 @@ def test_invalid_arguments_return_status(tm):
                                      1, 0, 0.1, null, 0, 8, 0, p, null, p,
                                      1 << 20, null)
     assert rc == tm._lib.TMOPT_EUNSUPPORTED
+    # decode: a ring table of 4 pages (64 positions) with no window, then
+    # with a window wider than the ring
+    for window in (0, 65):
+        rc = lib.tmopt_attn_decode_paged(p, p, p, p, 4, 4, p, 1, 32, 4, 128,
+                                         16, 1, window, 0.1, null, 0, 8, 0, p,
+                                         null, p, 1 << 20, null)
+        assert rc == tm._lib.TMOPT_EINVAL
+        assert b"ring of 4 pages" in lib.tmopt_last_error()
     # prefill: REP 3 is unsupported
     rc = lib.tmopt_attn_prefill_varlen(p, 0, 0, p, 0, 0, p, 0, 0, p, null, 1,
                                        4, null, null, null, 0, 16, 0, 12, 4,

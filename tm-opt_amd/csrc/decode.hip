@@ -680,6 +680,12 @@ extern "C" int tmopt_attn_decode_paged(
                 "decode: num_pages=%lld bt_stride=%lld table_wrap=%d",
                 (long long)num_pages, (long long)bt_stride, table_wrap);
   TMOPT_REQUIRE(window >= 0, TMOPT_EINVAL, "decode: window=%d", window);
+  // a ring table holds the last table_wrap * 16 positions: a wider (or no)
+  // window would read rows the ring has already overwritten
+  TMOPT_REQUIRE(table_wrap == 0 ||
+                    (window > 0 && (int64_t)window <= (int64_t)table_wrap * kPS),
+                TMOPT_EINVAL, "decode: window=%d outside a ring of %d pages",
+                window, table_wrap);
   TMOPT_REQUIRE(min_pages > 0 && num_workgroups >= 0, TMOPT_EINVAL,
                 "decode: min_pages=%d num_workgroups=%d", min_pages,
                 num_workgroups);

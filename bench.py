@@ -126,6 +126,38 @@ def bench_prefill(tm, wl, window, steps, warmup, n_sets=2):
     }
 
 
+def bench_kv_write(tm, wl, steps, warmup, n_sets=2):
+    """Config 4's KV-cache write: the 8 runs' K/V appended from position 0
+    through a shuffled block table (pool = 2x the pages needed). Bytes =
+    2 (K, V) x (read + write) x T x HKV x D x 2 + 8 per token."""
+    c0 = wl.config4(window=0, device="cuda")
+    T, HKV, D = c0.k.shape
+    g = torch.Generator().manual_seed(c0.meta["seed"])
+    table, P = wl.paged_layout(c0.lens, g)
+    table = table.to("cuda")
+    start = torch.zeros(len(c0.lens), dtype=torch.int32, device="cuda")
+    sets = [(torch.empty((P, 16, HKV, D), dtype=torch.bfloat16,
+                         device="cuda"),
+             torch.empty((P, 16, HKV, D), dtype=torch.bfloat16,
+                         device="cuda")) for _ in range(n_sets)]
+    max_len = max(c0.lens)
+
+    def fn(pools):
+        tm.kv_write_paged(c0.k, c0.v, table, start, pools[0], pools[1],
+                          cu_seqlens=c0.cu_seqlens, max_seqlen=max_len)
+
+    wall, mean_ms = time_launches(fn, sets, steps, warmup)
+    nbytes = 2 * 2 * T * HKV * D * 2 + T * 8
+    return {
+        "workload": "C4_kv_write_paged", "tokens": T,
+        "bytes_per_launch": nbytes, "ms_per_step": wall * 1e3 / steps,
+        "us_per_launch_events": mean_ms * 1e3,
+        "gbs_events": nbytes / (mean_ms * 1e-3) / 1e9,
+        "roofline_frac": nbytes / (mean_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "seed": c0.meta["seed"],
+    }
+
+
 def _event_ms(fn, reps):
     fn()
     torch.cuda.synchronize()
@@ -305,6 +337,10 @@ def main():
                   f" us {r['tflops_events']:.0f} TFLOP/s", file=sys.stderr,
                   flush=True)
             extra["C4_prefill_" + ("global" if win == 0 else f"swa{win}")] = r
+        r = bench_kv_write(tm, wl, args.steps, args.warmup)
+        print(f"[bench] C4 kv write {r['us_per_launch_events']:.1f} us "
+              f"{r['gbs_events']:.0f} GB/s", file=sys.stderr, flush=True)
+        extra["C4_kv_write"] = r
     if args.only in ("", "c5"):
         r = bench_mixed(tm, wl, max(3, args.steps // 10), 2)
         print(f"[bench] C5 step {r['ms_per_step_graph']:.2f} ms "

@@ -193,3 +193,25 @@ def test_rising_scores_rescale(tm, dev, window):
         out, lse = _run(tm, case, dev, min_pages=mp, num_workgroups=wgs)
         assert_out_close(out, ref_o, f"rising w={window} mp={mp}")
         assert_lse_close(lse, ref_l, f"rising w={window} mp={mp}")
+
+
+@pytest.mark.parametrize("window", [0, 64])
+def test_batch_above_one_scan_pass(tm, dev, window):
+    """B = 700: the start-up prefix scan over the batch runs in passes of
+    256 sequences, each carrying the previous passes' total. Lengths 0-300
+    (zero-length rows at every 50th sequence), so most sequences are one or
+    two pages and many work-group boundaries fall inside the second and
+    third passes."""
+    from importlib import import_module
+    wl = import_module("tm-opt_amd.workloads")
+    B = 700
+    ctx = [0 if b % 50 == 0 else 1 + (b * 37) % 300 for b in range(B)]
+    case = wl.make_decode("big-b", 13, B, 0, 0, window=window, ctx=ctx)
+    ref_o, ref_l = _oracle(case)
+    for mp, wgs in ((1, 0), (3, 97)):
+        out, lse = _run(tm, case, dev, min_pages=mp, num_workgroups=wgs)
+        what = f"B=700 window={window} min_pages={mp} wgs={wgs}"
+        assert_out_close(out, ref_o, what)
+        assert_lse_close(lse, ref_l, what)
+        zero = torch.tensor([c == 0 for c in ctx])
+        assert torch.all(out[zero].float() == 0), what

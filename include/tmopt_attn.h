@@ -94,7 +94,9 @@ int tmopt_kv_write_slots(const void* k, const void* v, int64_t k_stride_tok,
  * (the decode step). max_seqlen bounds the per-sequence token count, and
  * max_seqlen * HKV * D / 8 must stay below 2^31 (TMOPT_EINVAL otherwise);
  * positions are int32.
- * Table entries outside [0, num_pages) are skipped, never dereferenced.
+ * Table entries outside [0, num_pages) are skipped, never dereferenced,
+ * and so are tokens whose logical page lies past the row width (index >=
+ * bt_stride).
  */
 int tmopt_kv_write_paged(const void* k, const void* v, int64_t k_stride_tok,
                          int64_t k_stride_head, int64_t v_stride_tok,
@@ -140,7 +142,8 @@ size_t tmopt_attn_decode_workspace_size(int B, int HQ, int HKV, int D,
  *               sequence b is block_table[b*bt_stride + (table_wrap ?
  *               lp % table_wrap : lp)]. Only pages holding visible keys are
  *               read; entries outside [0, num_pages) are never dereferenced
- *               (their keys count as absent).
+ *               and a logical page past the row width (index >= bt_stride)
+ *               has no entry: the keys of both count as absent.
  * ctx_lens:     [B] int32 keys in the cache including the current token
  *               (0 = empty: output 0, LSE -inf).
  * window:       0 = global; W > 0 = sliding window, keys k with
@@ -186,20 +189,36 @@ int tmopt_attn_decode_paged(const void* q, const void* k_pool,
  * runs. Replaces _attn_prefill_kernel
  * (engine/pyengine/kernels/attn_prefill.py:71-141) behind attn_prefill_fused
  * (attn_prefill.py:144-194); the padded [B,H,T,D] form becomes cu_seqlens
- * packing, and chunked prefill reads prior context from the paged cache.
+ * packing, and chunked prefill (the seam the reference leaves at
+ * Engine.prefill, engine/pyengine/scheduler.py:22-23) reads prior context
+ * from the paged cache or the sliding-window ring.
  *
  * q:      [total_q, HQ, D] with element strides (q_stride_tok,
  *         q_stride_head), D contiguous. Query j of sequence i (row
  *         cu_seqlens_q[i] + j) sits at position prior_lens[i] + j
  *         (prior_lens NULL = all zero).
  * Keys of sequence i are positions [0, prior_lens[i] + len_i). They come
- * from one of two sources:
- *   block_table == NULL: packed k, v [total_q, HKV, D] (strides as q) hold
- *         the run's own keys; prior_lens must be NULL.
- *   block_table != NULL: every key is read from the paged pools
- *         (k_pool, v_pool, [num_pages, page_size, HKV, D]) through
- *         block_table [num_seqs, bt_stride]; the run's new keys must already
- *         be written (tmopt_kv_write_paged), k and v are ignored.
+ * from one of three sources:
+ *   block_table == NULL (packed): k, v [total_q, HKV, D] (strides as q)
+ *         hold the run's own keys; prior_lens and table_wrap must be 0.
+ *   block_table != NULL, k == v == NULL (paged): every key is read from
+ *         the paged pools (k_pool, v_pool, [num_pages, page_size, HKV, D])
+ *         through block_table [num_seqs, bt_stride]; the run's new keys
+ *         must already be written (tmopt_kv_write_paged). table_wrap = 0.
+ *   block_table != NULL, k, v given (mixed): keys before prior_lens[i]
+ *         from the pools, the run's own keys from packed k / v. The run's
+ *         keys need not be in the pool yet: append them afterwards. With
+ *         table_wrap > 0 each table row is a ring of table_wrap pages
+ *         holding the last table_wrap * page_size positions (RingKV /
+ *         SwaPool, engine/pyengine/kv.py:66-114, :215-235); then
+ *         0 < window <= table_wrap * page_size, and the append must come
+ *         after this call (it overwrites the ring).
+ * Pool reads: logical page lp of sequence i is block_table[i * bt_stride +
+ *         (table_wrap ? lp % table_wrap : lp)]; a page past the row width
+ *         (index >= bt_stride) or with an entry outside [0, num_pages)
+ *         reads as zeros. Rows before the first key a query block may see
+ *         (window) are never read, so a windowed table may point pages
+ *         wholly before the window at any page, poisoned or not.
  * window: 0 = causal; W > 0 adds pos_q - pos_k < W. Key tiles wholly
  *         outside the causal/window band are skipped.
  * scale:  softmax scale (> 0).
@@ -209,13 +228,18 @@ int tmopt_attn_decode_paged(const void* q, const void* k_pool,
  *         that band get 0 (attn_prefill.py:115-120). Rows must not overlap
  *         (rel_stride_tok >= rel_extent) and 32 rows must span less than
  *         2 GiB, else TMOPT_EUNSUPPORTED.
- * A run's q rows (and, on the packed source, its k / v rows) must span less
+ * A run's q rows (and, with packed keys, its k / v rows) must span less
  * than 2 GiB (max_seqlen_q * stride): TMOPT_EUNSUPPORTED otherwise.
  * max_seqlen_q bounds every len_i (it sizes the grid).
  * out:    [total_q, HQ, D] with element strides (o_stride_tok,
  *         o_stride_head), D contiguous.
  * lse:    [HQ, total_q] fp32 natural-log sum-exp of the scaled scores, or
  *         NULL.
+ * reject: optional device int32 (NULL = none). When it holds a nonzero
+ *         value at launch, every output row and LSE entry the launch owns
+ *         is written as NaN and no key is read: a caller that validated its
+ *         inputs on the device (e.g. attn_prefill_fused's positions must
+ *         be an arange) fails loudly without a host synchronisation.
  */
 int tmopt_attn_prefill_varlen(
     const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k,
@@ -223,10 +247,11 @@ int tmopt_attn_prefill_varlen(
     int64_t v_stride_tok, int64_t v_stride_head, const int32_t* cu_seqlens_q,
     const int32_t* prior_lens, int num_seqs, int max_seqlen_q,
     const void* k_pool, const void* v_pool, const int32_t* block_table,
-    int64_t bt_stride, int page_size, int64_t num_pages, int HQ, int HKV, int D,
-    int window, float scale, const void* rel, int64_t rel_stride_tok,
-    int64_t rel_stride_head, int rel_extent, void* out, int64_t o_stride_tok,
-    int64_t o_stride_head, float* lse, tmopt_stream_t stream);
+    int64_t bt_stride, int table_wrap, int page_size, int64_t num_pages,
+    int HQ, int HKV, int D, int window, float scale, const void* rel,
+    int64_t rel_stride_tok, int64_t rel_stride_head, int rel_extent,
+    void* out, int64_t o_stride_tok, int64_t o_stride_head, float* lse,
+    const int32_t* reject, tmopt_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -65,21 +65,21 @@ def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
         pages, offs = _key_rows(bt[b], pos, table_wrap)
         K = k_pool[pages, offs].float()            # [n_vis, HKV, D]
         V = v_pool[pages, offs].float()
-        Kh = K.repeat_interleave(rep, dim=1)       # [n_vis, HQ, D]
-        Vh = V.repeat_interleave(rep, dim=1)
-        qb = q[b].float()                          # [HQ, D]
-        s = torch.einsum("hd,nhd->hn", qb, Kh) * scale
+        # head h = kvh * REP + r reads KV head kvh: group the query heads
+        qb = q[b].float().view(HKV, rep, D)        # [HKV, REP, D]
+        s = torch.matmul(qb, K.permute(1, 2, 0)).reshape(HQ, -1) * scale
         if rel is not None:
             s = s + rel_bias_gather(rel[b].cpu(), (n - 1) - pos)
         lse[b] = torch.logsumexp(s, dim=-1)
-        p = torch.softmax(s, dim=-1)
-        out[b] = torch.einsum("hn,nhd->hd", p, Vh)
+        p = torch.softmax(s, dim=-1)               # [HQ, n_vis]
+        out[b] = torch.matmul(p.view(HKV, rep, -1),
+                              V.permute(1, 0, 2)).reshape(HQ, D)
     return out, lse
 
 
 def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, prior_lens=None,
                    k_pool=None, v_pool=None, block_table=None, q_block=256,
-                   rel=None):
+                   rel=None, table_wrap=0):
     """Causal (optionally windowed) attention over packed runs.
 
     Follows _attn_prefill_kernel (engine/pyengine/kernels/attn_prefill.py:
@@ -87,9 +87,12 @@ def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, prior_lens=None,
     530-556): query j of run i sits at position p_i + j (p_i = prior tokens),
     keys at positions 0..p_i+len_i-1, kept iff 0 <= qpos - kpos (< W on
     windowed layers) — the additive_causal_mask predicate (model.py:228-246).
-    GQA head h reads KV head h // REP. Prior keys (and, when block_table is
-    given, all keys) come from the paged pools through the table; otherwise
-    the run's own keys are the packed k/v rows.
+    GQA head h reads KV head h // REP. With a block table and no k/v every
+    key comes from the paged pools (PagedKV.gather, kv.py:207-212); with a
+    block table and k/v the prior keys come from the pools (a ring of
+    table_wrap pages when table_wrap > 0: RingKV slot p % W, kv.py:75-76,
+    :105-114) and the run's own keys from the packed rows; without a table
+    every key is a packed row (no prior context).
     rel (optional, [total, HQ, E]): query row t of head h adds
     rel[t, h, qpos - kpos] to the scaled score inside 0 <= qpos - kpos < E
     and nothing outside (attn_prefill.py:114-120, rel_bias model.py:137-158).
@@ -98,7 +101,7 @@ def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, prior_lens=None,
     total, HQ, D = q.shape
     cu = cu_seqlens.to(torch.int64).cpu()
     S = cu.shape[0] - 1
-    if block_table is not None:
+    if block_table is not None and k is None:
         HKV = k_pool.shape[2]
     else:
         HKV = k.shape[1]
@@ -112,11 +115,25 @@ def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, prior_lens=None,
             continue
         p0 = 0 if prior_lens is None else int(prior_lens[i])
         nk = p0 + T
-        if block_table is not None:
+        if block_table is not None and k is None:
+            assert not table_wrap, "a ring holds the prior context only"
             kpos = torch.arange(nk, dtype=torch.int64)
             pages, offs = _key_rows(block_table[i].cpu(), kpos, 0)
             K = k_pool[pages, offs].float()
             V = v_pool[pages, offs].float()
+        elif block_table is not None:
+            # prior keys the window can reach (a ring keeps the last W only;
+            # older positions are never visible to this run's queries)
+            lo = max(0, p0 - window + 1) if window else 0
+            kpos = torch.arange(lo, p0, dtype=torch.int64)
+            pages, offs = _key_rows(block_table[i].cpu(), kpos, table_wrap)
+            HKV_ = k.shape[1]
+            K = torch.zeros((nk, HKV_, D), dtype=torch.float32)
+            V = torch.zeros((nk, HKV_, D), dtype=torch.float32)
+            K[lo:p0] = k_pool[pages, offs].float()
+            V[lo:p0] = v_pool[pages, offs].float()
+            K[p0:] = k[t0:t1].float()
+            V[p0:] = v[t0:t1].float()
         else:
             assert p0 == 0
             K = k[t0:t1].float()

@@ -47,7 +47,11 @@ def write_paged(pool, rows, cu_seqlens, start_pos, block_table, page=PAGE,
     start_pos[i] + t. With a ring table only the last table_wrap * page
     positions of a run can survive; earlier ones are dropped as
     RingKV.append drops them (engine/pyengine/kv.py:94-98). Entries outside
-    the pool are skipped. cu_seqlens None = one token per run."""
+    the pool are skipped, and so are tokens whose logical page lies past the
+    table row's width (the reference's tables always cover the appended
+    positions, PagedKV.ensure_pages kv.py:170-191; the native write treats
+    a too-short row as absent entries). cu_seqlens None = one token per
+    run."""
     H, D = rows.shape[1], rows.shape[2]
     flat = pool.reshape(-1, H, D)
     n_pages = flat.shape[0] // page
@@ -67,6 +71,8 @@ def write_paged(pool, rows, cu_seqlens, start_pos, block_table, page=PAGE,
             lp = p // page
             if table_wrap:
                 lp %= table_wrap
+            if lp >= len(block_table[i]):
+                continue
             pg = int(block_table[i][lp])
             if not 0 <= pg < n_pages:
                 continue

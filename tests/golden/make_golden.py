@@ -125,6 +125,84 @@ def prefill_case(rng, name, lens, HQ, HKV, D, window):
             "q": q, "k": k, "v": v, "out": out, "lse": lse}
 
 
+def prefill_paged_case(rng, name, prior, lens, HQ, HKV, D, window, wrap=0):
+    """Chunked prefill: run i's queries sit at positions prior[i] + j and
+    see keys 0 .. prior[i] + j. Keys before prior[i] live in a shuffled
+    page pool through a block table (a ring of `wrap` pages holding the
+    last 16 * wrap positions when wrap > 0, as RingKV keeps them); the
+    run's own keys are the packed k / v rows. Without a ring the pool also
+    holds the run's own keys (the same values), so the case serves the
+    all-paged source as well."""
+    rep = HQ // HKV
+    total = sum(lens)
+    cu = [0]
+    for t in lens:
+        cu.append(cu[-1] + t)
+    q = tensor(rng, total, HQ, D)
+    k = tensor(rng, total, HKV, D)
+    v = tensor(rng, total, HKV, D)
+    S = len(lens)
+    n_pages = [wrap if wrap else (prior[i] + lens[i] + PAGE - 1) // PAGE
+               for i in range(S)]
+    width = max(n_pages)
+    P = sum(n_pages) + 2
+    ids = list(range(P))
+    rng.shuffle(ids)
+    table, off = [], 0
+    for i in range(S):
+        row = ids[off:off + n_pages[i]] + [-1] * (width - n_pages[i])
+        off += n_pages[i]
+        table.append(row)
+    k_pool = tensor(rng, P, PAGE, HKV, D)
+    v_pool = tensor(rng, P, PAGE, HKV, D)
+
+    def row_of(i, p):
+        lp = p // PAGE
+        if wrap:
+            lp %= wrap
+        return table[i][lp], p % PAGE
+
+    # the pool's content: prior keys (random), plus the run's own keys when
+    # the table is not a ring (then the paged source reads them there)
+    pk = {}
+    for i in range(S):
+        last = prior[i] if wrap else prior[i] + lens[i]
+        first = max(0, prior[i] - wrap * PAGE) if wrap else 0
+        for p in range(first, last):
+            pg, o = row_of(i, p)
+            if p >= prior[i]:
+                kv = (k[cu[i] + p - prior[i]], v[cu[i] + p - prior[i]])
+            else:
+                kv = (tensor(rng, HKV, D), tensor(rng, HKV, D))
+            k_pool[pg][o], v_pool[pg][o] = kv
+            pk[(i, p)] = kv
+    scale = 0.125
+    out = [[None] * HQ for _ in range(total)]
+    lse = [[None] * total for _ in range(HQ)]
+    for i, T in enumerate(lens):
+        for j in range(T):
+            pos = prior[i] + j
+            lo = max(0, pos - window + 1) if window else 0
+            for h in range(HQ):
+                kh = h // rep
+                keys, vals = [], []
+                for p in range(lo, pos + 1):
+                    if p < prior[i]:
+                        kv = pk[(i, p)]
+                    else:
+                        kv = (k[cu[i] + p - prior[i]], v[cu[i] + p - prior[i]])
+                    keys.append(kv[0][kh])
+                    vals.append(kv[1][kh])
+                o, l = attend(q[cu[i] + j][h], keys, vals, scale)
+                out[cu[i] + j][h] = o
+                lse[h][cu[i] + j] = l
+    return {"name": name, "kind": "prefill_paged", "lens": lens,
+            "prior": prior, "cu": cu, "HQ": HQ, "HKV": HKV, "D": D,
+            "window": window, "table_wrap": wrap, "scale": scale,
+            "block_table": table, "k_pool": k_pool, "v_pool": v_pool,
+            "q": q, "k": k, "v": v, "out": out, "lse": lse}
+
+
 def kv_write_case(rng, name):
     """Paged append of three runs (start positions 0, 5, 30; lengths 7, 20,
     3) through a shuffled table; expected pool after the write."""
@@ -192,6 +270,14 @@ def main():
         prefill_case(rng, "prefill_causal", [1, 4, 9, 40], 8, 1, 128, 0),
         prefill_case(rng, "prefill_window3", [6, 10], 4, 1, 128, 3),
         kv_write_case(rng, "kv_write_paged"),
+    ]
+    # a generator of its own, so the cases above keep their values
+    rng2 = random.Random(20261202)
+    cases += [
+        prefill_paged_case(rng2, "prefill_paged_prior", [0, 5, 16, 40],
+                           [3, 17, 1, 33], 8, 2, 128, 0),
+        prefill_paged_case(rng2, "prefill_ring_window20", [10, 50, 33],
+                           [5, 40, 2], 8, 2, 128, 20, wrap=2),
     ]
     for c in cases:
         for key in INPUTS:

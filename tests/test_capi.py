@@ -73,10 +73,27 @@ def test_invalid_arguments_return_status(tm):
         assert b"ring of 4 pages" in lib.tmopt_last_error()
     # prefill: REP 3 is unsupported
     rc = lib.tmopt_attn_prefill_varlen(p, 0, 0, p, 0, 0, p, 0, 0, p, null, 1,
-                                       4, null, null, null, 0, 16, 0, 12, 4,
-                                       128, 0, 0.1, null, 0, 0, 0, p, 0, 0,
-                                       null, null)
+                                       4, null, null, null, 0, 0, 16, 0, 12,
+                                       4, 128, 0, 0.1, null, 0, 0, 0, p, 0, 0,
+                                       null, null, null)
     assert rc == tm._lib.TMOPT_EUNSUPPORTED
+
+    def prefill(k, prior, table, wrap, window):
+        return lib.tmopt_attn_prefill_varlen(
+            p, 4096, 128, k, 512, 128, k, 512, 128, p, prior, 1, 64, p, p,
+            table, 8, wrap, 16, 100, 32, 4, 128, window, 0.1, null, 0, 0, 0,
+            p, 4096, 128, null, null, null)
+    # prefill: a ring table needs the run's own k/v (mixed source) and a
+    # window no wider than the ring; prior context needs a block table
+    for k, window in ((null, 64), (p, 0), (p, 129)):
+        assert prefill(k, p, p, 8, window) == tm._lib.TMOPT_EINVAL
+        assert b"ring table" in lib.tmopt_last_error()
+    rc = lib.tmopt_attn_prefill_varlen(
+        p, 4096, 128, p, 512, 128, p, 512, 128, p, p, 1, 64, null, null,
+        null, 0, 0, 16, 0, 32, 4, 128, 0, 0.1, null, 0, 0, 0, p, 4096, 128,
+        null, null, null)
+    assert rc == tm._lib.TMOPT_EINVAL
+    assert b"prior context needs a block table" in lib.tmopt_last_error()
     # kv write: misaligned strides
     rc = lib.tmopt_kv_write_slots(p, p, 3, 8, 8, 8, p, 1, 4, 128, p, p, 10,
                                   null)

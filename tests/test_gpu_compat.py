@@ -94,3 +94,30 @@ def test_attn_prefill_fused_padded_batch(tm, dev, window, E, hq, hk):
     torch.cuda.synchronize()
     assert out.shape == (B, T, hq, D)
     assert_out_close(out, ref, f"prefill_fused w={window} {hq}/{hk}")
+
+
+def test_attn_prefill_fused_positions(tm, dev):
+    """Positions: any common offset p0 + arange(T) gives the arange result
+    (the mask and bias depend on q - k only); anything else is rejected on
+    the device (NaN output, no host synchronisation) and on the host for
+    CPU position tensors."""
+    g = torch.Generator().manual_seed(16)
+    B, T, D, hq, hk, E = 2, 100, 128, 32, 4, 64
+    q = torch.randn((B, hq, T, D), generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn((B, hk, T, D), generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn((B, hk, T, D), generator=g).to(torch.bfloat16).to(dev)
+    rel = torch.randn((B, hq, T, E), generator=g).to(torch.bfloat16).to(dev)
+    ar = torch.arange(T, device=dev)
+    base = tm.attn_prefill_fused(q, k, v, rel, ar, ar, E)
+    off = tm.attn_prefill_fused(q, k, v, rel, ar + 4096, ar + 4096, E)
+    torch.cuda.synchronize()
+    assert torch.isfinite(base.float()).all()
+    assert torch.equal(base, off)
+    bad_q = ar.clone()
+    bad_q[50] += 1
+    for qp, kp in ((bad_q, ar), (ar, ar + 1), (ar.flip(0), ar.flip(0))):
+        out = tm.attn_prefill_fused(q, k, v, rel, qp, kp, E)
+        torch.cuda.synchronize()
+        assert torch.isnan(out.float()).all()
+    with pytest.raises(AssertionError):
+        tm.attn_prefill_fused(q, k, v, rel, bad_q.cpu(), ar.cpu(), E)

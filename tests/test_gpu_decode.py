@@ -215,3 +215,29 @@ def test_batch_above_one_scan_pass(tm, dev, window):
         assert_lse_close(lse, ref_l, what)
         zero = torch.tensor([c == 0 for c in ctx])
         assert torch.all(out[zero].float() == 0), what
+
+
+def test_row_width_bound(tm, dev):
+    """ctx_lens reaching past a block-table row: the logical pages beyond
+    the row's width count as absent (the result is the attention over the
+    keys the row covers), never the next row's pages, which are NaN."""
+    g = torch.Generator().manual_seed(71)
+    HQ, HKV, D, P = 32, 4, 128, 10
+    kp = torch.randn((P, 16, HKV, D), generator=g).to(torch.bfloat16)
+    vp = torch.randn((P, 16, HKV, D), generator=g).to(torch.bfloat16)
+    kp[6:] = float("nan")
+    vp[6:] = float("nan")
+    table = torch.tensor([[1, 4, 0, 3], [6, 7, 8, 9]], dtype=torch.int32)
+    q = torch.randn((2, HQ, D), generator=g).to(torch.bfloat16)
+    ctx = torch.tensor([100, 0], dtype=torch.int32)   # row 0 covers 64 keys
+    for mp, wgs in ((1, 0), (2, 3)):
+        out, lse = tm.decode_paged(q.to(dev), kp.to(dev), vp.to(dev),
+                                   table.to(dev), ctx.to(dev), 0.1,
+                                   min_pages=mp, num_workgroups=wgs)
+        torch.cuda.synchronize()
+        # the covered keys 0..63 seen from query position 99 (no window, no
+        # bias: the position enters nowhere else)
+        ref_o, ref_l = attn_ref.decode_paged(q[:1], kp, vp, table[:1],
+                                             torch.tensor([64]), 0.1)
+        assert_out_close(out[:1], ref_o, "row width")
+        assert_lse_close(lse[:1], ref_l, "row width")

@@ -57,3 +57,27 @@ def test_kv_write_golden(tm, dev):
     torch.cuda.synchronize()
     assert np.array_equal(kv_ref.as_u16(pool),
                           kv_ref.as_u16(c["want"].to(torch.bfloat16)))
+
+
+@pytest.mark.parametrize("c", golden.cases("prefill_paged"),
+                         ids=lambda c: c["name"])
+def test_prefill_paged_golden(tm, dev, c):
+    """Chunked prefill against the brute force: prior keys from a shuffled
+    page pool (or a ring of 2 pages under a window of 20, with a 40-token
+    chunk longer than the ring), the run's own keys from the pool (paged
+    source) or from packed k/v (mixed source)."""
+    table = torch.tensor(c["block_table"], dtype=torch.int32, device=dev)
+    prior = torch.tensor(c["prior"], dtype=torch.int32, device=dev)
+    cu = torch.tensor(c["cu"], dtype=torch.int32, device=dev)
+    sources = ("mixed",) if c["table_wrap"] else ("paged", "mixed")
+    for source in sources:
+        own = source == "mixed"
+        out, lse = tm.prefill_varlen(
+            c["q"].to(dev), c["k"].to(dev) if own else None,
+            c["v"].to(dev) if own else None, cu, c["scale"],
+            window=c["window"], prior_lens=prior,
+            k_pool=c["k_pool"].to(dev), v_pool=c["v_pool"].to(dev),
+            block_table=table, table_wrap=c["table_wrap"])
+        torch.cuda.synchronize()
+        assert_out_close(out, c["out"], f"{c['name']} {source}")
+        assert_lse_close(lse, c["lse"], f"{c['name']} {source}")

@@ -206,3 +206,122 @@ def test_write_paged_long_runs_and_single_tokens(tm, dev, wrap):
     torch.cuda.synchronize()
     assert np.array_equal(kv_ref.as_u16(kd), want_k)
     assert np.array_equal(kv_ref.as_u16(vd), want_v)
+
+
+def _chunks_per_lane(max_len, num_seqs, HKV=4, D=128):
+    """The launch's chunks-per-lane rule (kv_write.hip): the smallest power
+    of two up to 16 that keeps (max_len * HKV * D / 8) / (256 R) x num_seqs
+    within 32768 work-groups."""
+    work = max_len * HKV * D // 8
+    R = 1
+    while True:
+        bx = -(-work // (256 * R))
+        if R == 16 or bx == 1 or bx * num_seqs <= 32768:
+            return R
+        R *= 2
+
+
+@pytest.mark.parametrize("n_single,want_r", [(99, 4), (199, 8), (399, 16)])
+@pytest.mark.parametrize("wrap", [0, 200])
+def test_write_paged_many_chunks_per_lane(tm, dev, n_single, want_r, wrap):
+    """A 4096-token run beside hundreds of one-token rows (a mixed step at
+    real batch sizes): the launch packs 4, 8 or 16 chunks per lane; every
+    token must land bit-exact, with and without a ring table (a ring of 200
+    pages = 3200 positions, so the long run's first 896 tokens are dropped
+    as RingKV.append drops them)."""
+    assert _chunks_per_lane(4096, n_single + 1) == want_r
+    g = torch.Generator().manual_seed(40 + n_single + wrap)
+    H, D = 4, 128
+    lens = [4096] + [1] * n_single
+    S = len(lens)
+    start = [int(x) for x in torch.randint(0, 5000, (S,), generator=g)]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    k = _bf16((T, H, D), g)
+    v = _bf16((T, H, D), g)
+    # distinct pages for the table entries a run writes, -1 elsewhere
+    used = []
+    for s0, n in zip(start, lens):
+        keep = max(s0, s0 + n - wrap * 16) if wrap else s0
+        lps = {p // 16 for p in range(keep, s0 + n)}
+        used.append(sorted({lp % wrap for lp in lps} if wrap else lps))
+    width = wrap if wrap else max(u[-1] + 1 for u in used)
+    P = sum(len(u) for u in used) + 3
+    perm = torch.randperm(P, generator=g).to(torch.int32)
+    table = torch.full((S, width), -1, dtype=torch.int32)
+    off = 0
+    for i, u in enumerate(used):
+        table[i, u] = perm[off:off + len(u)]
+        off += len(u)
+    kp = _bf16((P, 16, H, D), g)
+    vp = _bf16((P, 16, H, D), g)
+    want_k = kv_ref.write_paged(kv_ref.as_u16(kp).copy(), kv_ref.as_u16(k),
+                                cu, start, table.numpy(), 16, wrap)
+    want_v = kv_ref.write_paged(kv_ref.as_u16(vp).copy(), kv_ref.as_u16(v),
+                                cu, start, table.numpy(), 16, wrap)
+    kd, vd = kp.to(dev), vp.to(dev)
+    tm.kv_write_paged(k.to(dev), v.to(dev), table.to(dev),
+                      torch.tensor(start, dtype=torch.int32, device=dev), kd,
+                      vd, cu_seqlens=torch.from_numpy(cu).to(dev),
+                      table_wrap=wrap)
+    torch.cuda.synchronize()
+    assert np.array_equal(kv_ref.as_u16(kd), want_k)
+    assert np.array_equal(kv_ref.as_u16(vd), want_v)
+
+
+def test_config4_full_append(tm, dev):
+    """BASELINE config 4's KV-cache write at full size (8 runs, 21,970
+    tokens from position 0 through a shuffled table, pool = 2x the pages),
+    as bench.py times it; the whole pool compared bit-exact."""
+    from importlib import import_module
+    wl = import_module("tm-opt_amd.workloads")
+    c = wl.config4(window=0)
+    T, H, D = c.k.shape
+    assert T == sum(c.lens) and len(c.lens) == 8
+    g = torch.Generator().manual_seed(c.meta["seed"])
+    table, P = wl.paged_layout(c.lens, g)
+    kp = torch.zeros((P, 16, H, D), dtype=torch.bfloat16)
+    vp = torch.zeros_like(kp)
+    cu = c.cu_seqlens.numpy()
+    start = np.zeros(len(c.lens), dtype=np.int32)
+    want_k = kv_ref.write_paged(kv_ref.as_u16(kp).copy(), kv_ref.as_u16(c.k),
+                                cu, start, table.numpy())
+    want_v = kv_ref.write_paged(kv_ref.as_u16(vp).copy(), kv_ref.as_u16(c.v),
+                                cu, start, table.numpy())
+    kd, vd = kp.to(dev), vp.to(dev)
+    tm.kv_write_paged(c.k.to(dev), c.v.to(dev), table.to(dev),
+                      torch.from_numpy(start).to(dev), kd, vd,
+                      cu_seqlens=c.cu_seqlens.to(dev),
+                      max_seqlen=max(c.lens))
+    torch.cuda.synchronize()
+    assert np.array_equal(kv_ref.as_u16(kd), want_k)
+    assert np.array_equal(kv_ref.as_u16(vd), want_v)
+
+
+def test_write_paged_row_width_bound(tm, dev):
+    """A run whose positions reach past its table row: the tokens of pages
+    beyond the row's width are skipped, and the next row's pages (which a
+    read past the row would find) stay untouched."""
+    g = torch.Generator().manual_seed(51)
+    H, D, P = 4, 128, 16
+    k = _bf16((40, H, D), g)
+    v = _bf16((40, H, D), g)
+    table = torch.tensor([[3, 9], [5, 12]], dtype=torch.int32)  # 2 pages/row
+    cu = np.array([0, 40], dtype=np.int32)      # run 0: positions 0..39
+    start = np.array([0], dtype=np.int32)
+    kp = _bf16((P, 16, H, D), g)
+    vp = _bf16((P, 16, H, D), g)
+    want_k = kv_ref.write_paged(kv_ref.as_u16(kp).copy(), kv_ref.as_u16(k),
+                                cu, start, table.numpy())
+    want_v = kv_ref.write_paged(kv_ref.as_u16(vp).copy(), kv_ref.as_u16(v),
+                                cu, start, table.numpy())
+    kd, vd = kp.to(dev), vp.to(dev)
+    tm.kv_write_paged(k.to(dev), v.to(dev), table.to(dev),
+                      torch.from_numpy(start).to(dev), kd, vd,
+                      cu_seqlens=torch.from_numpy(cu).to(dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(kv_ref.as_u16(kd), want_k)
+    assert np.array_equal(kv_ref.as_u16(vd), want_v)
+    # positions 32..39 (logical page 2) were skipped: pages 5 and 12 intact
+    assert torch.equal(kd[5].cpu(), kp[5]) and torch.equal(kd[12].cpu(),
+                                                          kp[12])

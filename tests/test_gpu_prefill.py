@@ -313,3 +313,205 @@ def test_score_spike_underflows_old_terms(tm, dev):
     out, lse = _gpu(tm, case, dev)
     assert_out_close(out, ref_o, "spike")
     assert_lse_close(lse, ref_l, "spike")
+
+
+def _chunked_pool(g, lens, prior, HKV, D, poison_before=None, nan_page=False,
+                  extra_pages=0):
+    """Shuffled page pool holding every key (prior context + each run's own
+    tokens) of the runs; positions before poison_before[i] hold NaN rows
+    and, with nan_page, table entries of pages wholly before it point at a
+    NaN page (as a windowed table may). Returns (k_pool, v_pool, table,
+    k_all, v_all) with k_all[i] the run's keys in position order."""
+    wl = _wl()
+    table, P = wl.paged_layout(lens, g, pool_factor=2, prior=prior)
+    P += 1 + extra_pages
+    tot = [p + t for p, t in zip(prior, lens)]
+    kp = torch.full((P, 16, HKV, D), float("nan"), dtype=torch.bfloat16)
+    vp = torch.full((P, 16, HKV, D), float("nan"), dtype=torch.bfloat16)
+    k_all, v_all = [], []
+    for i in range(len(lens)):
+        ka = torch.randn((tot[i], HKV, D), generator=g).to(torch.bfloat16)
+        va = torch.randn((tot[i], HKV, D), generator=g).to(torch.bfloat16)
+        if poison_before is not None:
+            ka[:poison_before[i]] = float("nan")
+            va[:poison_before[i]] = float("nan")
+        pos = torch.arange(tot[i])
+        pages = table[i][pos // 16].long()
+        kp[pages, pos % 16] = ka
+        vp[pages, pos % 16] = va
+        if nan_page and poison_before is not None:
+            table[i, :poison_before[i] // 16] = P - 1 - extra_pages
+        k_all.append(ka)
+        v_all.append(va)
+    return kp, vp, table, k_all, v_all
+
+
+def _packed_own(k_all, lens, prior):
+    return torch.cat([ka[p:p + t] for ka, p, t in zip(k_all, prior, lens)])
+
+
+@pytest.mark.parametrize("source", ["paged", "mixed"])
+@pytest.mark.parametrize("hq,hkv", [(32, 4), (64, 16)])
+def test_window_never_reads_before_it(tm, dev, source, hq, hkv):
+    """Windowed chunked prefill over a pool whose keys before each run's
+    first visible position (prior - W + 1) are NaN, pages wholly before it
+    mapped to a NaN page: the tile grid starts up to 63 keys (3 pages)
+    before the window, and those rows must never be read (a masked
+    probability of 0 times a NaN value is NaN)."""
+    g = torch.Generator().manual_seed(61)
+    W, D = 48, 128
+    prior = [300, 70, 49, 1000, 0]
+    lens = [90, 200, 1, 33, 64]
+    first = [max(0, p - W + 1) for p in prior]
+    kp, vp, table, k_all, v_all = _chunked_pool(g, lens, prior, hkv, D,
+                                                poison_before=first,
+                                                nan_page=True)
+    cu = torch.zeros(len(lens) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens), 0)
+    q = torch.randn((int(cu[-1]), hq, D), generator=g).to(torch.bfloat16)
+    pr = torch.tensor(prior, dtype=torch.int32)
+    k_own = _packed_own(k_all, lens, prior)
+    v_own = _packed_own(v_all, lens, prior)
+    ref_o, ref_l = attn_ref.prefill_varlen(q, k_own, v_own, cu, 0.08,
+                                           window=W, prior_lens=pr,
+                                           k_pool=kp, v_pool=vp,
+                                           block_table=table)
+    own = source == "mixed"
+    out, lse = tm.prefill_varlen(q.to(dev), k_own.to(dev) if own else None,
+                                 v_own.to(dev) if own else None, cu.to(dev),
+                                 0.08, window=W, prior_lens=pr.to(dev),
+                                 k_pool=kp.to(dev), v_pool=vp.to(dev),
+                                 block_table=table.to(dev))
+    torch.cuda.synchronize()
+    assert_out_close(out, ref_o, f"pre-window NaN {source} {hq}/{hkv}")
+    assert_lse_close(lse, ref_l, f"pre-window NaN {source} {hq}/{hkv}")
+
+
+@pytest.mark.parametrize("window", [0, 100])
+def test_mixed_source_equals_paged_bitwise(tm, dev, window):
+    """The mixed source (prior keys from the pool, the run's own from packed
+    rows) feeds the same bytes to the same tiles as the all-paged source
+    when the pool also holds the run's keys: the outputs are identical.
+    Priors of every residue mod 4 put the source boundary inside a 4-row
+    load block (split by exec mask)."""
+    g = torch.Generator().manual_seed(62)
+    HQ, HKV, D = 32, 4, 128
+    prior = [0, 1, 2, 3, 17, 250, 511, 64]
+    lens = [70, 33, 5, 129, 64, 300, 1, 66]
+    kp, vp, table, k_all, v_all = _chunked_pool(g, lens, prior, HKV, D)
+    cu = torch.zeros(len(lens) + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens), 0)
+    q = torch.randn((int(cu[-1]), HQ, D), generator=g).to(torch.bfloat16)
+    args = dict(window=window, prior_lens=torch.tensor(
+        prior, dtype=torch.int32, device=dev), k_pool=kp.to(dev),
+        v_pool=vp.to(dev), block_table=table.to(dev))
+    a = tm.prefill_varlen(q.to(dev), None, None, cu.to(dev), 0.08, **args)
+    b = tm.prefill_varlen(q.to(dev),
+                          _packed_own(k_all, lens, prior).to(dev),
+                          _packed_own(v_all, lens, prior).to(dev),
+                          cu.to(dev), 0.08, **args)
+    torch.cuda.synchronize()
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+    ref_o, ref_l = attn_ref.prefill_varlen(q, None, None, cu, 0.08,
+                                           window=window,
+                                           prior_lens=args["prior_lens"].cpu(),
+                                           k_pool=kp, v_pool=vp,
+                                           block_table=table)
+    assert_out_close(a[0], ref_o, f"mixed==paged w={window}")
+    assert_lse_close(a[1], ref_l, f"mixed==paged w={window}")
+
+
+@pytest.mark.parametrize("hq,hkv", [(64, 16), (32, 4)])
+def test_ring_prior_context_chunks_longer_than_window(tm, dev, hq, hkv):
+    """SWA chunked prefill over the reference's ring storage (SwaPool rows
+    [S + 1, W, HK, D], RingKV slot p % W): the ring holds each sequence's
+    last W positions before the chunk; the chunk's own keys come from
+    packed k/v (chunks up to 3x the ring), then the chunk is appended to
+    the ring and the ring state is checked bit-exact against RingKV's rule
+    (only the last W positions survive)."""
+    from oracle import kv_ref
+    import numpy as np
+    g = torch.Generator().manual_seed(63)
+    W, D = 512, 128
+    per = W // 16
+    prior = [0, 100, 511, 512, 513, 4000, 700]
+    lens = [300, 1500, 1, 700, 64, 520, 1]
+    S = len(lens)
+    slots = [4, 0, 6, 2, 1, 5, 3]
+    # ring state before the chunk: stale random rows everywhere, then each
+    # sequence's last min(prior, W) positions written at p % W
+    pool_k = torch.randn((S + 1, W, hkv, D), generator=g).to(torch.bfloat16)
+    pool_v = torch.randn((S + 1, W, hkv, D), generator=g).to(torch.bfloat16)
+    table = (torch.tensor(slots)[:, None] * per +
+             torch.arange(per)[None]).to(torch.int32)
+    cu = torch.zeros(S + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(torch.tensor(lens), 0)
+    T = int(cu[-1])
+    q = torch.randn((T, hq, D), generator=g).to(torch.bfloat16)
+    k = torch.randn((T, hkv, D), generator=g).to(torch.bfloat16)
+    v = torch.randn((T, hkv, D), generator=g).to(torch.bfloat16)
+    kp = pool_k.view((S + 1) * per, 16, hkv, D)
+    vp = pool_v.view((S + 1) * per, 16, hkv, D)
+    pr = torch.tensor(prior, dtype=torch.int32)
+    ref_o, ref_l = attn_ref.prefill_varlen(q, k, v, cu, 1.0 / D, window=W,
+                                           prior_lens=pr, k_pool=kp,
+                                           v_pool=vp, block_table=table,
+                                           table_wrap=per)
+    kd, vd = kp.to(dev), vp.to(dev)
+    out, lse = tm.prefill_varlen(q.to(dev), k.to(dev), v.to(dev), cu.to(dev),
+                                 1.0 / D, window=W, prior_lens=pr.to(dev),
+                                 k_pool=kd, v_pool=vd,
+                                 block_table=table.to(dev), table_wrap=per)
+    # then the append, after the attention (it overwrites the ring)
+    tm.kv_write_paged(k.to(dev), v.to(dev), table.to(dev), pr.to(dev), kd, vd,
+                      cu_seqlens=cu.to(dev), table_wrap=per)
+    torch.cuda.synchronize()
+    assert_out_close(out, ref_o, f"ring chunks {hq}/{hkv}")
+    assert_lse_close(lse, ref_l, f"ring chunks {hq}/{hkv}")
+    want = kv_ref.write_paged(kv_ref.as_u16(kp).copy(), kv_ref.as_u16(k),
+                              cu.numpy(), prior, table.numpy(), 16, per)
+    assert np.array_equal(kv_ref.as_u16(kd), want)
+
+
+def test_paged_row_width_bound(tm, dev):
+    """A block-table row narrower than the run's keys: the logical pages
+    past its width read as zero rows (score 0, value 0) instead of the next
+    row's pages, which hold NaN here."""
+    g = torch.Generator().manual_seed(64)
+    HQ, HKV, D = 32, 4, 128
+    P = 12
+    kp = torch.randn((P, 16, HKV, D), generator=g).to(torch.bfloat16)
+    vp = torch.randn((P, 16, HKV, D), generator=g).to(torch.bfloat16)
+    kp[7:] = float("nan")
+    vp[7:] = float("nan")
+    # run 0 needs 3 pages (40 keys) but its row holds 2; row 1 = NaN pages
+    table = torch.tensor([[2, 5], [7, 8]], dtype=torch.int32)
+    cu = torch.tensor([0, 40], dtype=torch.int32)
+    q = torch.randn((40, HQ, D), generator=g).to(torch.bfloat16)
+    out, lse = tm.prefill_varlen(q.to(dev), None, None, cu.to(dev), 0.1,
+                                 prior_lens=None, k_pool=kp.to(dev),
+                                 v_pool=vp.to(dev), block_table=table.to(dev))
+    torch.cuda.synchronize()
+    # expected: the third page is a zero page
+    kz = torch.cat([kp[:7], torch.zeros((1, 16, HKV, D),
+                                        dtype=torch.bfloat16)])
+    vz = torch.cat([vp[:7], torch.zeros((1, 16, HKV, D),
+                                        dtype=torch.bfloat16)])
+    ref_o, ref_l = attn_ref.prefill_varlen(
+        q, None, None, cu, 0.1, prior_lens=torch.zeros(1, dtype=torch.int32),
+        k_pool=kz, v_pool=vz, block_table=torch.tensor([[2, 5, 7]]))
+    assert_out_close(out, ref_o, "row width")
+    assert_lse_close(lse, ref_l, "row width")
+
+
+def test_reject_flag_writes_nan(tm, dev):
+    """A nonzero device reject flag turns every output row and LSE entry of
+    the launch into NaN; a zero flag changes nothing."""
+    case = _wl().make_prefill("rej", 26, lens=[70, 1, 300], window=0)
+    base = _gpu(tm, case, dev)
+    zero = torch.zeros(1, dtype=torch.int32, device=dev)
+    one = torch.ones(1, dtype=torch.int32, device=dev)
+    a = _gpu(tm, case, dev, reject=zero)
+    b = _gpu(tm, case, dev, reject=one)
+    assert torch.equal(a[0], base[0]) and torch.equal(a[1], base[1])
+    assert torch.isnan(b[0].float()).all() and torch.isnan(b[1]).all()

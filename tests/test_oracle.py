@@ -395,3 +395,91 @@ def test_varlen_bias_matches_padded_semantics():
         b, _ = attn_ref.prefill_varlen(pk(q), pk(k), pk(v), cu, 1.0 / D,
                                        window=window or 0, rel=pk(rel))
         assert (a.reshape(B * T, H, D) - b).abs().max() < 1e-5, window
+
+
+# --------------------------------------------------------------------------
+# chunked prefill: prior context from the paged pools / a ring
+# --------------------------------------------------------------------------
+
+def _prefill_paged_golden(c, source, prior_shift=0, wrap=None, window=None,
+                          q=None):
+    prior = torch.tensor(c["prior"], dtype=torch.int32) + prior_shift
+    table = torch.tensor(c["block_table"], dtype=torch.int64)
+    own = source == "mixed"
+    return attn_ref.prefill_varlen(
+        c["q"] if q is None else q, c["k"] if own else None,
+        c["v"] if own else None, torch.tensor(c["cu"]), c["scale"],
+        window=c["window"] if window is None else window, prior_lens=prior,
+        k_pool=c["k_pool"], v_pool=c["v_pool"], block_table=table,
+        table_wrap=c["table_wrap"] if wrap is None else wrap)
+
+
+def _paged_sources(c):
+    # a ring holds the prior context only: the mixed source alone reads it
+    return ("mixed",) if c["table_wrap"] else ("paged", "mixed")
+
+
+@pytest.mark.parametrize("c", golden.cases("prefill_paged"),
+                         ids=lambda c: c["name"])
+def test_prefill_paged_oracle_matches_golden(c):
+    """The oracle's prior-context branches (all keys from the pools; prior
+    keys from the pools or a ring and the run's own from packed rows)
+    against the plain-Python brute force."""
+    for source in _paged_sources(c):
+        out, lse = _prefill_paged_golden(c, source)
+        assert _close(out, c["out"]) and _close(lse, c["lse"]), source
+
+
+@pytest.mark.parametrize("c", golden.cases("prefill_paged"),
+                         ids=lambda c: c["name"])
+def test_prefill_paged_planted_mistakes(c):
+    """Plausible mistakes in the prior-context branch each fail the golden
+    comparison: query positions off by one, the ring wrap ignored, the
+    window one wider."""
+    muts = {"prior_plus_1": dict(prior_shift=1)}
+    if c["table_wrap"]:
+        muts["no_ring_wrap"] = dict(wrap=0)
+    if c["window"]:
+        muts["window_plus_1"] = dict(window=c["window"] + 1)
+    for name, kw in muts.items():
+        for source in _paged_sources(c):
+            try:
+                out, lse = _prefill_paged_golden(c, source, **kw)
+            except (IndexError, RuntimeError):
+                continue          # an out-of-table read also catches it
+            caught = not (_close(out, c["out"]) and _close(lse, c["lse"]))
+            assert caught, f"planted mistake {name} ({source}) passed"
+
+
+@pytest.mark.parametrize("c", golden.cases("prefill_paged"),
+                         ids=lambda c: c["name"])
+def test_prefill_paged_zero_query_closed_form(c):
+    """q = 0: uniform weights over the visible keys, so LSE = ln(number of
+    visible keys) = ln(min(prior + j + 1, W)) whatever the keys, the table
+    or the ring, and out = the mean of the visible V rows."""
+    q0 = torch.zeros_like(c["q"])
+    W = c["window"]
+    for source in _paged_sources(c):
+        out, lse = _prefill_paged_golden(c, source, q=q0)
+        want = []
+        for p, T in zip(c["prior"], c["lens"]):
+            n = torch.arange(p + 1, p + T + 1, dtype=torch.float64)
+            want.append(torch.log(torch.clamp(n, max=W) if W else n))
+        want = torch.cat(want)[None].expand(lse.shape[0], -1)
+        assert (lse.double() - want).abs().max() < 1e-5, source
+    # the mean of V: run 0, last query, head 0, through the brute-force rows
+    out, _ = _prefill_paged_golden(c, _paged_sources(c)[-1], q=q0)
+    i, T, p0 = 0, c["lens"][0], c["prior"][0]
+    pos = p0 + T - 1
+    lo = max(0, pos - W + 1) if W else 0
+    rows = []
+    for p in range(lo, pos + 1):
+        if p < p0:
+            lp = p // 16
+            if c["table_wrap"]:
+                lp %= c["table_wrap"]
+            rows.append(c["v_pool"][c["block_table"][i][lp], p % 16, 0])
+        else:
+            rows.append(c["v"][c["cu"][i] + p - p0, 0])
+    want = torch.stack(rows).float().mean(0)
+    assert (out[c["cu"][i] + T - 1, 0] - want).abs().max() < 1e-5

@@ -72,6 +72,9 @@ def kv_write_paged(k, v, block_table, start_pos, k_pool, v_pool,
     assert start_pos.dtype == torch.int32
     S = start_pos.shape[0]
     assert block_table.shape[0] >= S
+    # the kernel bounds every row read by the stride: rows must be whole
+    assert block_table.stride(0) == block_table.shape[1] or S <= 1, \
+        "block-table rows must be whole (the row width is the stride)"
     if cu_seqlens is None:
         assert T == S, (T, S)
         max_seqlen = 1
@@ -121,7 +124,8 @@ def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
     > 0 = each table row is a ring of that many pages (SWA ring pools).
     rel: optional [B, HQ, E] bf16 fused relative bias (attn_swa.py:97-102).
     min_pages / num_workgroups: work-split knobs (see the C header).
-    workspace: from decode_workspace() (allocated and zeroed if None).
+    workspace: from decode_workspace() (allocated if None; it needs no
+    initialisation).
     Returns (out [B, HQ, D] bf16, lse [B, HQ] fp32).
     Reference: engine/pyengine/kernels/attn_swa.py:49-141,
     attn_global.py:15-38."""
@@ -134,6 +138,9 @@ def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
     assert Dk == D and HQ % HKV == 0, (k_pool.shape, q.shape)
     assert block_table.dtype == torch.int32 and block_table.dim() == 2
     assert block_table.stride(1) == 1 and block_table.shape[0] >= B
+    # the kernel bounds every row read by the stride: rows must be whole
+    assert block_table.stride(0) == block_table.shape[1] or B <= 1, \
+        "block-table rows must be whole (the row width is the stride)"
     assert ctx_lens.dtype == torch.int32 and ctx_lens.shape == (B,)
     if rel is not None:
         assert rel.dtype == torch.bfloat16 and rel.is_contiguous()
@@ -165,19 +172,28 @@ def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
 
 def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, max_seqlen=None,
                    prior_lens=None, k_pool=None, v_pool=None,
-                   block_table=None, rel=None, out=None, lse=None,
-                   return_lse=True):
+                   block_table=None, table_wrap=0, rel=None, out=None,
+                   lse=None, return_lse=True, reject=None):
     """Varlen causal (optionally windowed) prefill attention on bf16 MFMA.
 
-    q [total, HQ, D], k/v [total, HKV, D] bf16 (D contiguous, any token /
-    head strides); cu_seqlens [S+1] int32. With block_table (int32
-    [S, bt_stride]) every key, prior context included, is read from
-    k_pool/v_pool [num_pages, 16, HKV, D] and prior_lens [S] int32 gives the
-    position of each run's first query; the run's own keys must already be
-    in the pool. rel: optional fused relative bias [total, HQ, E] (last
-    axis contiguous, any token/head strides): pair (q, k) of head h adds
-    rel[q_row, h, pos_q - pos_k] inside 0 <= dist < E (attn_prefill.py:
-    115-120). Returns (out [total, HQ, D] bf16, lse [HQ, total] fp32 or None).
+    q [total, HQ, D] bf16 (D contiguous, any token / head strides);
+    cu_seqlens [S+1] int32. Query j of run i sits at position
+    prior_lens[i] + j. Key sources:
+      * block_table None: k/v [total, HKV, D] hold each run's own keys
+        (no prior context);
+      * block_table given, k/v None: every key, prior context included, is
+        read from k_pool/v_pool [num_pages, 16, HKV, D] through block_table
+        (int32 [S, bt_stride]); the run's own keys must already be there;
+      * block_table and k/v given: prior keys from the pools, the run's own
+        keys from k/v. table_wrap > 0 makes each table row a ring of that
+        many pages (a sliding-window pool: 0 < window <= 16 * table_wrap,
+        and the run must be appended to the ring after this call).
+    rel: optional fused relative bias [total, HQ, E] (last axis contiguous,
+    any token/head strides): pair (q, k) of head h adds rel[q_row, h,
+    pos_q - pos_k] inside 0 <= dist < E (attn_prefill.py:115-120).
+    reject: optional int32 device scalar; nonzero -> NaN outputs (device-side
+    input rejection without a host sync).
+    Returns (out [total, HQ, D] bf16, lse [HQ, total] fp32 or None).
     Reference: engine/pyengine/kernels/attn_prefill.py:71-194."""
     total, HQ, D = q.shape
     _check_rows(q, "q")
@@ -185,46 +201,61 @@ def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, max_seqlen=None,
     S = cu_seqlens.shape[0] - 1
     if max_seqlen is None:
         max_seqlen = int((cu_seqlens[1:] - cu_seqlens[:-1]).max()) if S else 0
-    paged = block_table is not None
-    if paged:
+    pooled = block_table is not None
+    own = k is not None or v is not None
+    if pooled:
         assert k_pool is not None and v_pool is not None
         assert k_pool.is_contiguous() and v_pool.is_contiguous()
         assert k_pool.shape == v_pool.shape and k_pool.dim() == 4
         P, page_size, HKV, Dk = k_pool.shape
         assert Dk == D
         assert block_table.dtype == torch.int32 and block_table.stride(1) == 1
+        assert block_table.dim() == 2 and block_table.shape[0] >= S
+        assert block_table.stride(0) == block_table.shape[1] or S <= 1, \
+            "block-table rows must be whole (the row width is the stride)"
         if prior_lens is not None:
             assert prior_lens.dtype == torch.int32 and prior_lens.shape == (S,)
-        ks = vs = (0, 0)
+        if table_wrap:
+            assert own, "a ring table needs the run's own k/v (mixed source)"
+            assert 0 < window <= table_wrap * page_size, \
+                "a ring table needs a window no wider than the ring"
     else:
         assert prior_lens is None, "prior context needs the paged source"
+        assert own, "the packed source needs k and v"
+        assert not table_wrap
+        P, page_size = 0, PAGE_SIZE
+    ks = vs = (0, 0)
+    if own:
         assert k is not None and v is not None
         _check_rows(k, "k")
         _check_rows(v, "v")
         assert k.shape[0] == total and v.shape == k.shape and k.shape[2] == D
+        if pooled:
+            assert k.shape[1] == HKV
         HKV = k.shape[1]
-        P, page_size = 0, PAGE_SIZE
         ks = (k.stride(0), k.stride(1))
         vs = (v.stride(0), v.stride(1))
     assert HQ % HKV == 0
     if rel is not None:
         assert rel.dtype == torch.bfloat16 and rel.stride(2) == 1
         assert rel.shape[:2] == (total, HQ), (rel.shape, total, HQ)
+    if reject is not None:
+        assert reject.dtype == torch.int32 and reject.numel() >= 1
     dev = q.device
     if out is None:
         out = torch.empty((total, HQ, D), dtype=torch.bfloat16, device=dev)
     if lse is None and return_lse:
         lse = torch.empty((HQ, total), dtype=torch.float32, device=dev)
     _lib.call("tmopt_attn_prefill_varlen", _ptr(q), q.stride(0), q.stride(1),
-              None if paged else _ptr(k), ks[0], ks[1],
-              None if paged else _ptr(v), vs[0], vs[1], _ptr(cu_seqlens),
+              _ptr(k) if own else None, ks[0], ks[1],
+              _ptr(v) if own else None, vs[0], vs[1], _ptr(cu_seqlens),
               _ptr(prior_lens), S, int(max_seqlen),
-              _ptr(k_pool) if paged else None,
-              _ptr(v_pool) if paged else None, _ptr(block_table),
-              block_table.stride(0) if paged else 0, page_size, P, HQ, HKV,
-              D, int(window), float(scale), _ptr(rel),
+              _ptr(k_pool) if pooled else None,
+              _ptr(v_pool) if pooled else None, _ptr(block_table),
+              block_table.stride(0) if pooled else 0, int(table_wrap),
+              page_size, P, HQ, HKV, D, int(window), float(scale), _ptr(rel),
               0 if rel is None else rel.stride(0),
               0 if rel is None else rel.stride(1),
               0 if rel is None else rel.shape[2], _ptr(out), out.stride(0),
-              out.stride(1), _ptr(lse), _stream(dev))
+              out.stride(1), _ptr(lse), _ptr(reject), _stream(dev))
     return out, lse

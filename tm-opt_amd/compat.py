@@ -99,12 +99,20 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
     assert H % HK == 0
     if window is not None:
         assert E == window, (E, window)
-    if q_positions.device.type == "cpu" or os.environ.get("TMOPT_CHECK"):
-        # positions are derived in-kernel from indices: both must be arange
-        ar = torch.arange(T, device=q_positions.device)
-        assert torch.equal(q_positions, ar) and torch.equal(
-            kv_positions.to(ar.device), ar), "positions must be arange(T)"
     dev = q.device
+    # The kernel derives positions from indices, i.e. it computes with
+    # q_positions == kv_positions == p0 + arange(T) for any common p0 (the
+    # mask and the bias depend on q - k only); that is what the engine
+    # passes (model.py:526-528). Anything else is rejected: on the device
+    # the check feeds the kernel's reject flag (NaN output, no host sync),
+    # on the host (CPU positions, or TMOPT_CHECK set) it raises.
+    pos = torch.stack([q_positions, kv_positions.to(q_positions.device)])
+    ar = torch.arange(T, device=pos.device)
+    bad = ((pos - q_positions[:1]) != ar).any()
+    if pos.device.type == "cpu" or os.environ.get("TMOPT_CHECK"):
+        assert not bool(bad), \
+            "q_positions and kv_positions must be the same p0 + arange(T)"
+    reject = bad.to(device=dev, dtype=torch.int32).reshape(1)
     qp = _packed(q, B, T, H, D)
     kp = _packed(k, B, T, HK, D)
     vp = _packed(v, B, T, HK, D)
@@ -117,5 +125,5 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
     attn.prefill_varlen(qp, kp, vp, cu, 1.0 / D,
                         window=0 if window is None else int(window),
                         max_seqlen=T, rel=relp, out=out.view(B * T, H, D),
-                        return_lse=False)
+                        return_lse=False, reject=reject)
     return out

@@ -76,6 +76,7 @@ struct DecodeArgs {
   const __bf16* vpool;
   const int32_t* bt;
   int64_t bt_stride;
+  int bt_width;      // entries a row may be read at: min(bt_stride, 2^31-1)
   int table_wrap;
   const int32_t* ctx_lens;
   int B, HQ, HKV;
@@ -104,6 +105,9 @@ __device__ __forceinline__ int vis_pages(int n, int window) {
 
 __device__ __forceinline__ int page_id(const DecodeArgs& a, int b, int lp) {
   const int idx = a.table_wrap > 0 ? lp % a.table_wrap : lp;
+  // a logical page past the row's width has no entry: its keys are absent
+  // (reading on would return the next row's page ids)
+  if ((unsigned)idx >= (unsigned)a.bt_width) return -1;
   const int v = as_const(a.bt)[(int64_t)b * a.bt_stride + idx];
   // one unsigned 32-bit compare: stays on the scalar unit (a 64-bit signed
   // compare would borrow VGPRs that in-flight loads may still own)
@@ -710,6 +714,7 @@ extern "C" int tmopt_attn_decode_paged(
   a.vpool = (const __bf16*)v_pool;
   a.bt = block_table;
   a.bt_stride = bt_stride;
+  a.bt_width = bt_stride > 0x7fffffff ? 0x7fffffff : (int)bt_stride;
   a.table_wrap = table_wrap;
   a.ctx_lens = ctx_lens;
   a.B = B;

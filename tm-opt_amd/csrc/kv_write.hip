@@ -82,7 +82,9 @@ __global__ __launch_bounds__(256) void kv_write_paged_kernel(
     const bool live = tl < len && pos >= 0 && pos >= keep_from;
     int lp = live ? pos / page_size : 0;
     if (table_wrap > 0) lp %= table_wrap;
-    page[p] = trow[lp];
+    // a logical page past the row's width has no entry (reading on would
+    // return the next row's page ids): the token is skipped
+    page[p] = (int64_t)lp < bt_stride ? trow[lp] : -1;
     const int rem = live ? gid - tl * per_tok : 0;
     const int h = rem / D16;
     const int c = rem - h * D16;

@@ -82,7 +82,7 @@ __device__ __forceinline__ void dma_b128(i32x4 rsrc, uint32_t lds, int voff) {
       "s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
       :
       : "s"(lds), "v"(voff), "s"(rsrc)
-      : "memory");
+      : "memory", "m0");
 }
 
 // wait until at most N vector-memory loads of this wave are in flight
@@ -106,6 +106,8 @@ struct PrefillArgs {
   const __bf16* vpool;
   const int32_t* bt;
   int64_t bt_stride;
+  int bt_width;      // entries a row may be read at: min(bt_stride, 2^31-1)
+  int table_wrap;    // > 0: each table row is a ring of that many pages
   int num_pages;
   int page_size;
   int HQ, HKV;
@@ -119,6 +121,7 @@ struct PrefillArgs {
   const __bf16* rel; // optional fused relative bias, rows like q
   int64_t r_st, r_sh;
   int rel_extent;
+  const int32_t* reject;  // optional device flag: nonzero = write NaN
 };
 
 // Sum over the wave, wave-uniform: within each 16-lane row by DPP (xor 1,
@@ -208,8 +211,18 @@ __device__ __forceinline__ Work schedule(const PrefillArgs& a, int BQ,
   return w;  // not reached for i < total
 }
 
-template <int REP, bool REL, bool PAGED>
+// Where the keys of a run come from.
+enum Source : int {
+  kPacked = 0,  // the run's own rows of packed k / v (no prior context)
+  kPaged = 1,   // every key, prior and own, from the page pools
+  kMixed = 2,   // keys before prior_lens[i] from the pools (or a ring of
+                // pages), the run's own keys from packed k / v
+};
+
+template <int REP, bool REL, int SRC>
 __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
+  constexpr bool POOL = SRC != kPacked;   // some keys come from the pools
+  constexpr bool OWN = SRC != kPaged;     // the run's keys from packed k/v
   constexpr int BQ = 256 / REP;   // queries per work-group
   constexpr int QSUB = BQ / 32;   // 32-query sub-blocks per head
   extern __shared__ __align__(16) char smem[];
@@ -233,8 +246,10 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   const int qn = min(BQ, len - q0);
   const int pos_lo = prior + q0;              // first query position
   const int pos_hi = prior + q0 + qn - 1;     // last valid query position
-  int k_lo = a.window > 0 ? max(0, pos_lo - a.window + 1) : 0;
-  k_lo = (k_lo / kBN) * kBN;
+  // first key any query of the block may see; tiles start at a multiple of
+  // the tile width below it
+  const int kwin = a.window > 0 ? max(0, pos_lo - a.window + 1) : 0;
+  const int k_lo = (kwin / kBN) * kBN;
   const int k_hi = pos_hi + 1;                // exclusive
   const int ntiles = (k_hi - k_lo + kBN - 1) / kBN;
 
@@ -263,28 +278,69 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // no static LDS), a multiple of 256 as the fragment addressing assumes
   const uint32_t lds0 =
       (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)smem);
+  // packed rows of the run (keys 0.. of the run itself)
   i32x4 rk = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
-  int kst_b = 0, vst_b = 0, klane = 0, vlane = 0;
-  [[maybe_unused]] const int row_b = a.HKV * kD * 2;   // paged: token row
-  [[maybe_unused]] const int64_t page_b = (int64_t)kPage * row_b;
-  if constexpr (!PAGED) {
+  int kst_b = 0, vst_b = 0, klane_p = 0, vlane_p = 0;
+  if constexpr (OWN) {
     kst_b = (int)(a.k_st * 2);
     vst_b = (int)(a.v_st * 2);
     rk = make_rsrc(a.k + (int64_t)t0 * a.k_st + (int64_t)kvh * a.k_sh,
                    (uint32_t)(((int64_t)(len - 1) * a.k_st + kD) * 2));
     rv = make_rsrc(a.v + (int64_t)t0 * a.v_st + (int64_t)kvh * a.v_sh,
                    (uint32_t)(((int64_t)(len - 1) * a.v_st + kD) * 2));
-    klane = grp * kst_b + 16 * kchunk;
-    vlane = grp * vst_b + 16 * vchunk;
-  } else {
+    klane_p = grp * kst_b + 16 * kchunk;
+    vlane_p = grp * vst_b + 16 * vchunk;
+  }
+  // pool rows: keys below `plim` (all keys on the paged source, the prior
+  // context on the mixed one)
+  [[maybe_unused]] const int row_b = a.HKV * kD * 2;   // one token row
+  [[maybe_unused]] const int64_t page_b = (int64_t)kPage * row_b;
+  [[maybe_unused]] int klane = 0, vlane = 0;
+  if constexpr (POOL) {
     klane = grp * row_b + kvh * (kD * 2) + 16 * kchunk;
     vlane = grp * row_b + kvh * (kD * 2) + 16 * vchunk;
   }
   [[maybe_unused]] const int32_t __attribute__((address_space(4)))* trow =
-      PAGED ? as_const(a.bt) + (int64_t)seq * a.bt_stride : nullptr;
-  [[maybe_unused]] const int last_lp = (nk - 1) >> 4;
+      POOL ? as_const(a.bt) + (int64_t)seq * a.bt_stride : nullptr;
+  [[maybe_unused]] const int plim = SRC == kMixed ? prior : nk;
+
+  // Four pool rows key0..key0+3 (one page: key0 % 4 == 0) into LDS. The
+  // buffer resource covers only the page's rows in [kwin, plim): rows before
+  // the first key a query of the block may see and rows past the pool's
+  // part read as zeros and are never fetched (a ring page there holds an
+  // overwritten position, a windowed table may point it at a poison page),
+  // and so does a page whose table entry lies outside the pool or past the
+  // row's width. The lane offset is relative to the resource base, so the
+  // rows below it have negative offsets, i.e. out of range.
+  auto pool_dma = [&](int key0, uint32_t dk, uint32_t dv) {
+    if constexpr (POOL) {
+      const int lp = key0 >> 4;
+      const int col = a.table_wrap > 0 ? lp % a.table_wrap : lp;
+      const int pg = (unsigned)col < (unsigned)a.bt_width ? trow[col] : -1;
+      const int r_lo = min(kPage, max(0, kwin - kPage * lp));
+      const int r_hi = min(kPage, max(0, plim - kPage * lp));
+      const bool valid = (unsigned)pg < (unsigned)a.num_pages && r_hi > r_lo;
+      const uint32_t nrec = valid ? (uint32_t)((r_hi - r_lo) * row_b) : 0u;
+      const int64_t pofs = valid ? (int64_t)pg * page_b + r_lo * row_b : 0;
+      const int roff = ((key0 & (kPage - 1)) - r_lo) * row_b;
+      dma_b128(make_rsrc(reinterpret_cast<const char*>(a.kpool) + pofs, nrec),
+               dk, klane + roff);
+      dma_b128(make_rsrc(reinterpret_cast<const char*>(a.vpool) + pofs, nrec),
+               dv, vlane + roff);
+    }
+  };
+  // four packed rows j..j+3 of the run's own keys into LDS (rows past the
+  // run end are outside the resource: zeros)
+  auto own_dma = [&](int j, uint32_t dk, uint32_t dv) {
+    if constexpr (OWN) {
+      dma_b128(rk, dk, klane_p + j * kst_b);
+      dma_b128(rv, dv, vlane_p + j * vst_b);
+    }
+  };
 
   // issue tile `t` (index from k_lo) into LDS stage `st`: 4 instructions
+  // per wave (2 with the source split inside a 4-row block: one per source,
+  // each under the exec mask of the lanes whose row it holds)
   auto issue_tile = [&](int t, int st) {
     const int kt = k_lo + t * kBN;
     const uint32_t sb = lds0 + st * kStage;
@@ -292,26 +348,21 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     for (int i = 0; i < 2; ++i) {
       const int r0 = 4 * w + 32 * i;          // first row of the block
       const uint32_t dk = sb + r0 * kRowB, dv = dk + kTileB;
-      if constexpr (!PAGED) {
-        dma_b128(rk, dk, klane + (kt + r0) * kst_b);
-        dma_b128(rv, dv, vlane + (kt + r0) * vst_b);
+      const int key0 = kt + r0;
+      if constexpr (SRC == kPacked) {
+        own_dma(key0, dk, dv);
+      } else if constexpr (SRC == kPaged) {
+        pool_dma(key0, dk, dv);
       } else {
-        // the 4 rows lie in one page; its resource covers only the rows
-        // of the run (and nothing for a page id outside the pool)
-        const int key0 = kt + r0;
-        const int lp = key0 >> 4;
-        const int pg = lp <= last_lp ? trow[lp] : -1;
-        const bool valid = (unsigned)pg < (unsigned)a.num_pages;
-        const int rows = min(kPage, max(0, nk - kPage * lp));
-        const uint32_t nrec = valid ? (uint32_t)(rows * row_b) : 0u;
-        const int64_t pofs = valid ? (int64_t)pg * page_b : 0;
-        const int roff = (key0 & (kPage - 1)) * row_b;
-        dma_b128(make_rsrc(reinterpret_cast<const char*>(a.kpool) + pofs,
-                           nrec),
-                 dk, klane + roff);
-        dma_b128(make_rsrc(reinterpret_cast<const char*>(a.vpool) + pofs,
-                           nrec),
-                 dv, vlane + roff);
+        if (key0 + 4 <= plim) {
+          pool_dma(key0, dk, dv);
+        } else if (key0 >= plim) {
+          own_dma(key0 - plim, dk, dv);
+        } else {
+          // lane group grp holds row key0 + grp
+          if (key0 + grp < plim) pool_dma(key0, dk, dv);
+          else own_dma(key0 - plim, dk, dv);
+        }
       }
     }
   };
@@ -593,6 +644,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     __builtin_amdgcn_s_setprio(0);
   };
 
+  // A caller that found its inputs invalid on the device (without a host
+  // sync) sets *reject: every output row and LSE entry of the launch is then
+  // NaN and no key is read.
+  const bool rejected = a.reject != nullptr && as_const(a.reject)[0] != 0;
+  if (!rejected) {
   // ---- pipeline: 4 LDS stages, tiles issued three ahead -------------------
   // Slot 2t: group 0 multiplies tile t, group 1 does the softmax of tile t;
   // slot 2t+1: group 0 the softmax of tile t+1, group 1 multiplies tile t.
@@ -661,12 +717,15 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
       odd_end(t);
     }
   }
+  }  // !rejected
 
   // ---- finalise: l over both lane halves, normalise, store --------------
   const float l_tot = l_part + __shfl_xor(l_part, 32);
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  const float inv = rejected ? __builtin_nanf("") :
+                    l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   if (a.lse && h2 == 0 && qok)
     a.lse[(int64_t)head * as_const(a.cu)[a.S] + t0 + qi] =
+        rejected ? __builtin_nanf("") :
         l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : -INFINITY;
   // O^T goes through LDS (free after the last barrier) so that the global
   // stores are whole rows: the wave writes its 32 x 128 block query-major
@@ -710,32 +769,34 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   }
 }
 
+template <int REP, bool REL>
+void launch_src(const PrefillArgs& a, int src, dim3 grid, size_t lds,
+                hipStream_t st) {
+  if (src == kPacked)
+    hipLaunchKernelGGL((prefill_kernel<REP, REL, kPacked>), grid, dim3(512),
+                       lds, st, a);
+  else if (src == kPaged)
+    hipLaunchKernelGGL((prefill_kernel<REP, REL, kPaged>), grid, dim3(512),
+                       lds, st, a);
+  else
+    hipLaunchKernelGGL((prefill_kernel<REP, REL, kMixed>), grid, dim3(512),
+                       lds, st, a);
+}
+
 template <int REP>
-void launch(PrefillArgs a, int S, int max_seqlen, hipStream_t st) {
+void launch(PrefillArgs a, int src, int S, int max_seqlen, hipStream_t st) {
   constexpr int BQ = 256 / REP;
   a.nqb_max = (max_seqlen + BQ - 1) / BQ;
   // HKV * items-per-head work-groups, rounded up to whole XCD rounds
   const int64_t items = (int64_t)S * a.nqb_max;
   int64_t n = a.HKV * items;
   if (a.HKV <= 8 && 8 % a.HKV == 0) n = 8 * ((items + 8 / a.HKV - 1) / (8 / a.HKV));
-  dim3 grid((unsigned)n);
-  const bool paged = a.bt != nullptr;
+  const dim3 grid((unsigned)n);
   const size_t lds = kNStage * kStage;
-  if (a.rel) {
-    if (paged)
-      hipLaunchKernelGGL((prefill_kernel<REP, true, true>), grid, dim3(512),
-                         lds, st, a);
-    else
-      hipLaunchKernelGGL((prefill_kernel<REP, true, false>), grid, dim3(512),
-                         lds, st, a);
-  } else {
-    if (paged)
-      hipLaunchKernelGGL((prefill_kernel<REP, false, true>), grid, dim3(512),
-                         lds, st, a);
-    else
-      hipLaunchKernelGGL((prefill_kernel<REP, false, false>), grid,
-                         dim3(512), lds, st, a);
-  }
+  if (a.rel)
+    launch_src<REP, true>(a, src, grid, lds, st);
+  else
+    launch_src<REP, false>(a, src, grid, lds, st);
 }
 
 }  // namespace
@@ -749,10 +810,11 @@ extern "C" int tmopt_attn_prefill_varlen(
     int64_t v_stride_tok, int64_t v_stride_head, const int32_t* cu_seqlens_q,
     const int32_t* prior_lens, int num_seqs, int max_seqlen_q,
     const void* k_pool, const void* v_pool, const int32_t* block_table,
-    int64_t bt_stride, int page_size, int64_t num_pages, int HQ, int HKV, int D,
-    int window, float scale, const void* rel, int64_t rel_stride_tok,
-    int64_t rel_stride_head, int rel_extent, void* out, int64_t o_stride_tok,
-    int64_t o_stride_head, float* lse, tmopt_stream_t stream) {
+    int64_t bt_stride, int table_wrap, int page_size, int64_t num_pages,
+    int HQ, int HKV, int D, int window, float scale, const void* rel,
+    int64_t rel_stride_tok, int64_t rel_stride_head, int rel_extent,
+    void* out, int64_t o_stride_tok, int64_t o_stride_head, float* lse,
+    const int32_t* reject, tmopt_stream_t stream) {
   clear_error();
   if (num_seqs == 0 || max_seqlen_q == 0) return TMOPT_OK;
   TMOPT_REQUIRE(num_seqs > 0 && num_seqs <= 65535 && max_seqlen_q > 0,
@@ -786,19 +848,37 @@ extern "C" int tmopt_attn_prefill_varlen(
                   "prefill: %lld work-groups exceed the grid limit",
                   (long long)blocks);
   }
-  const bool paged = block_table != nullptr;
-  if (paged) {
+  const bool pooled = block_table != nullptr;
+  const bool own = k != nullptr || v != nullptr;
+  const int src = !pooled ? kPacked : (own ? kMixed : kPaged);
+  if (pooled) {
     TMOPT_REQUIRE(k_pool && v_pool && page_size > 0 && bt_stride > 0 &&
-                      num_pages > 0,
+                      num_pages > 0 && table_wrap >= 0,
                   TMOPT_EINVAL,
                   "prefill: paged source needs pools, page_size, bt_stride");
     TMOPT_REQUIRE(page_size == kPage, TMOPT_EUNSUPPORTED,
                   "prefill: page_size=%d (only 16)", page_size);
     TMOPT_REQUIRE(((uintptr_t)k_pool | (uintptr_t)v_pool) % 16 == 0,
                   TMOPT_EINVAL, "prefill: pools must be 16-byte aligned");
+    TMOPT_REQUIRE((int64_t)kPage * HKV * kD * 2 < (1ll << 31),
+                  TMOPT_EUNSUPPORTED, "prefill: page too large");
+    // A ring holds the last table_wrap * 16 positions: the run's own keys
+    // would overwrite the prior context they must be read beside, so a
+    // ring is read for the prior context only (mixed source), under a
+    // window no wider than the ring.
+    TMOPT_REQUIRE(table_wrap == 0 ||
+                      (src == kMixed && table_wrap <= bt_stride && window > 0 &&
+                       (int64_t)window <= (int64_t)table_wrap * kPage),
+                  TMOPT_EINVAL,
+                  "prefill: a ring table (table_wrap=%d) needs packed k/v for "
+                  "the run's own keys and 0 < window <= %lld",
+                  table_wrap, (long long)table_wrap * kPage);
   } else {
-    TMOPT_REQUIRE(k && v && prior_lens == nullptr, TMOPT_EINVAL,
-                  "prefill: packed source needs k/v and no prior context");
+    TMOPT_REQUIRE(prior_lens == nullptr && table_wrap == 0, TMOPT_EINVAL,
+                  "prefill: prior context needs a block table");
+  }
+  if (own) {
+    TMOPT_REQUIRE(k && v, TMOPT_EINVAL, "prefill: k and v go together");
     TMOPT_REQUIRE(((int64_t)max_seqlen_q * (k_stride_tok > v_stride_tok
                                                 ? k_stride_tok
                                                 : v_stride_tok) +
@@ -834,6 +914,8 @@ extern "C" int tmopt_attn_prefill_varlen(
   a.vpool = (const __bf16*)v_pool;
   a.bt = block_table;
   a.bt_stride = bt_stride;
+  a.bt_width = bt_stride > 0x7fffffff ? 0x7fffffff : (int)bt_stride;
+  a.table_wrap = table_wrap;
   a.num_pages = num_pages > 0x7fffffff ? 0x7fffffff : (int)num_pages;
   a.page_size = page_size > 0 ? page_size : 16;
   a.HQ = HQ;
@@ -849,10 +931,11 @@ extern "C" int tmopt_attn_prefill_varlen(
   a.r_st = rel_stride_tok;
   a.r_sh = rel_stride_head;
   a.rel_extent = rel ? rel_extent : 0;
+  a.reject = reject;
   hipStream_t st = (hipStream_t)stream;
   if (rep == 8)
-    launch<8>(a, num_seqs, max_seqlen_q, st);
+    launch<8>(a, src, num_seqs, max_seqlen_q, st);
   else
-    launch<4>(a, num_seqs, max_seqlen_q, st);
+    launch<4>(a, src, num_seqs, max_seqlen_q, st);
   return check_launch("prefill");
 }

@@ -180,6 +180,36 @@ int tmopt_attn_decode_paged(const void* q, const void* k_pool,
                             void* out, float* lse, void* workspace,
                             size_t workspace_bytes, tmopt_stream_t stream);
 
+/*
+ * tmopt_attn_decode_paged without the workspace argument: the same kernels
+ * and results, with the scratch taken from a static device array inside the
+ * library (16 MiB per GPU, held until the process ends). This entry point
+ * has no counterpart in the reference; it is for callers that cannot
+ * allocate device memory: code under hipGraph stream capture, tight serving
+ * loops, harnesses that forbid hipMalloc. It calls no hipMalloc / hipFree
+ * and no allocating library routine.
+ *   - Launch shapes whose workspace (tmopt_attn_decode_workspace_size)
+ *     exceeds 16 MiB return TMOPT_EWORKSPACE (e.g. (B + num_workgroups) *
+ *     HQ above ~32,000).
+ *   - Every call on one GPU shares that GPU's array: calls that overlap on
+ *     one GPU (concurrent streams, or graphs replayed concurrently) race.
+ *     Calls in stream order do not: the scratch needs no clearing between
+ *     calls (every slot a call reads, that call writes first).
+ *   - The first call on a device resolves the array's device address
+ *     (hipGetSymbolAddress); make it outside stream capture.
+ */
+int tmopt_attn_decode_paged_noalloc(const void* q, const void* k_pool,
+                                    const void* v_pool,
+                                    const int32_t* block_table,
+                                    int64_t bt_stride, int table_wrap,
+                                    const int32_t* ctx_lens, int B, int HQ,
+                                    int HKV, int D, int page_size,
+                                    int64_t num_pages, int window, float scale,
+                                    const void* rel, int rel_extent,
+                                    int min_pages, int num_workgroups,
+                                    void* out, float* lse,
+                                    tmopt_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Varlen causal prefill attention (bf16 MFMA)                              */
 /* ------------------------------------------------------------------------ */

@@ -16,13 +16,15 @@ importlib.import_module("tm-opt_amd").
 from . import _lib
 from ._lib import TmoptError, TmoptLibraryMissing, version
 from .attn import (HEAD_DIM, PAGE_SIZE, decode_default_workgroups,
-                   decode_paged, decode_workspace, decode_workspace_size,
-                   kv_write_paged, kv_write_slots, prefill_varlen)
+                   decode_paged, decode_paged_noalloc, decode_workspace,
+                   decode_workspace_size, kv_write_paged, kv_write_slots,
+                   prefill_varlen)
 from .compat import attn_global, attn_prefill_fused, attn_swa
 
 __all__ = [
     "TmoptError", "TmoptLibraryMissing", "version", "HEAD_DIM", "PAGE_SIZE",
-    "decode_default_workgroups", "decode_paged", "decode_workspace",
+    "decode_default_workgroups", "decode_paged", "decode_paged_noalloc",
+    "decode_workspace",
     "decode_workspace_size", "kv_write_paged", "kv_write_slots",
     "prefill_varlen", "attn_swa", "attn_global", "attn_prefill_fused",
 ]

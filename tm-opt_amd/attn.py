@@ -113,22 +113,8 @@ def decode_workspace(B, HQ, HKV, device, num_workgroups=0):
     return torch.empty(max(n, 16), dtype=torch.uint8, device=device)
 
 
-def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
-                 table_wrap=0, rel=None, min_pages=8, num_workgroups=0,
-                 out=None, lse=None, workspace=None, return_lse=True):
-    """Split-KV paged decode attention (one launch, persistent grid).
-
-    q [B, HQ, D] bf16 contiguous (query at position ctx_lens[b]-1);
-    k_pool/v_pool [num_pages, 16, HKV, D] bf16 contiguous; block_table
-    [B, bt_stride] int32; ctx_lens [B] int32; window 0 = global; table_wrap
-    > 0 = each table row is a ring of that many pages (SWA ring pools).
-    rel: optional [B, HQ, E] bf16 fused relative bias (attn_swa.py:97-102).
-    min_pages / num_workgroups: work-split knobs (see the C header).
-    workspace: from decode_workspace() (allocated if None; it needs no
-    initialisation).
-    Returns (out [B, HQ, D] bf16, lse [B, HQ] fp32).
-    Reference: engine/pyengine/kernels/attn_swa.py:49-141,
-    attn_global.py:15-38."""
+def _decode_check(q, k_pool, v_pool, block_table, ctx_lens, window,
+                  table_wrap, rel):
     B, HQ, D = q.shape
     assert q.dtype == torch.bfloat16 and q.is_contiguous()
     assert k_pool.is_contiguous() and v_pool.is_contiguous()
@@ -148,6 +134,39 @@ def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
     if table_wrap:
         assert 0 < window <= table_wrap * page_size, \
             "a ring table needs a window no wider than the ring"
+    return B, HQ, D, P, page_size, HKV
+
+
+def _decode_common_args(q, k_pool, v_pool, block_table, ctx_lens, scale,
+                        window, table_wrap, rel, min_pages, num_workgroups,
+                        dims):
+    B, HQ, D, P, page_size, HKV = dims
+    return (_ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(block_table),
+            block_table.stride(0), int(table_wrap), _ptr(ctx_lens), B, HQ,
+            HKV, D, page_size, P, int(window), float(scale), _ptr(rel),
+            0 if rel is None else rel.shape[2], int(min_pages),
+            int(num_workgroups))
+
+
+def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
+                 table_wrap=0, rel=None, min_pages=8, num_workgroups=0,
+                 out=None, lse=None, workspace=None, return_lse=True):
+    """Split-KV paged decode attention (one launch, persistent grid).
+
+    q [B, HQ, D] bf16 contiguous (query at position ctx_lens[b]-1);
+    k_pool/v_pool [num_pages, 16, HKV, D] bf16 contiguous; block_table
+    [B, bt_stride] int32; ctx_lens [B] int32; window 0 = global; table_wrap
+    > 0 = each table row is a ring of that many pages (SWA ring pools).
+    rel: optional [B, HQ, E] bf16 fused relative bias (attn_swa.py:97-102).
+    min_pages / num_workgroups: work-split knobs (see the C header).
+    workspace: from decode_workspace() (allocated if None; it needs no
+    initialisation).
+    Returns (out [B, HQ, D] bf16, lse [B, HQ] fp32).
+    Reference: engine/pyengine/kernels/attn_swa.py:49-141,
+    attn_global.py:15-38."""
+    dims = _decode_check(q, k_pool, v_pool, block_table, ctx_lens, window,
+                         table_wrap, rel)
+    B, HQ, _, _, _, HKV = dims
     dev = q.device
     if out is None:
         out = torch.empty_like(q)
@@ -156,13 +175,35 @@ def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
     if workspace is None:
         workspace = decode_workspace(B, HQ, HKV, dev, num_workgroups)
     ws_bytes = workspace.numel() * workspace.element_size()
-    _lib.call("tmopt_attn_decode_paged", _ptr(q), _ptr(k_pool), _ptr(v_pool),
-              _ptr(block_table), block_table.stride(0), int(table_wrap),
-              _ptr(ctx_lens), B, HQ, HKV, D, page_size, P, int(window),
-              float(scale), _ptr(rel),
-              0 if rel is None else rel.shape[2], int(min_pages),
-              int(num_workgroups), _ptr(out), _ptr(lse), _ptr(workspace),
-              ws_bytes, _stream(dev))
+    _lib.call("tmopt_attn_decode_paged",
+              *_decode_common_args(q, k_pool, v_pool, block_table, ctx_lens,
+                                   scale, window, table_wrap, rel, min_pages,
+                                   num_workgroups, dims),
+              _ptr(out), _ptr(lse), _ptr(workspace), ws_bytes, _stream(dev))
+    return out, lse
+
+
+def decode_paged_noalloc(q, k_pool, v_pool, block_table, ctx_lens, scale,
+                         out, lse=None, window=0, table_wrap=0, rel=None,
+                         min_pages=8, num_workgroups=0):
+    """decode_paged through the allocation-free entry point: the scratch is
+    the library's static 16 MiB device buffer, so neither this call nor the
+    library allocates (out, and lse if wanted, are the caller's). Calls
+    that overlap on one GPU race on that buffer; launch shapes needing more
+    scratch raise (TMOPT_EWORKSPACE). No counterpart in the reference: for
+    callers that cannot allocate."""
+    dims = _decode_check(q, k_pool, v_pool, block_table, ctx_lens, window,
+                         table_wrap, rel)
+    assert out.shape == q.shape and out.dtype == torch.bfloat16
+    assert out.is_contiguous()
+    if lse is not None:
+        assert lse.dtype == torch.float32 and lse.is_contiguous()
+        assert lse.shape == q.shape[:2]
+    _lib.call("tmopt_attn_decode_paged_noalloc",
+              *_decode_common_args(q, k_pool, v_pool, block_table, ctx_lens,
+                                   scale, window, table_wrap, rel, min_pages,
+                                   num_workgroups, dims),
+              _ptr(out), _ptr(lse), _stream(q.device))
     return out, lse
 
 

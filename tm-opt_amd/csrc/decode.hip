@@ -51,6 +51,8 @@
 //  P.V: the A operand of lane (r, g) is dim 16 blk + r of tokens 4g..4g+3
 //  and 16+4g..16+4g+3 (two transposed reads), matching the P^T lane layout
 //  (element 4t + i <-> token 16t + 4g + i).
+#include <mutex>
+
 #include "common.h"
 
 namespace tmopt {
@@ -635,6 +637,40 @@ void launch(const DecodeArgs& a, int G, int nw, size_t lds, hipStream_t st) {
                        dim3(64 * nw), lds, st, a);
 }
 
+// ---- static scratch of the allocation-free entry point -------------------
+// Device memory for tmopt_attn_decode_paged_noalloc's workspace: a fixed
+// array in the library's code object, so the call needs no allocation.
+// Every GPU the library runs on holds its own copy until the process ends.
+constexpr size_t kScratchBytes = size_t(16) << 20;   // 16 MiB per GPU
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};
+
+// Device address of the current device's copy of `scratch`. The array's
+// name is a host-side stand-in in host code, never a device address: it is
+// resolved here, once per device with that device current, and only the
+// resolved address is passed to kernels.
+int scratch_address(void** addr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  TMOPT_REQUIRE(e == hipSuccess && dev >= 0 && dev < kMaxDevices,
+                TMOPT_ELAUNCH, "decode_noalloc: no current device (%s)",
+                hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    TMOPT_REQUIRE(e == hipSuccess && p != nullptr, TMOPT_ELAUNCH,
+                  "decode_noalloc: hipGetSymbolAddress failed on device %d: "
+                  "%s", dev, hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return TMOPT_OK;
+}
+
 }  // namespace
 }  // namespace tmopt
 
@@ -749,4 +785,32 @@ extern "C" int tmopt_attn_decode_paged(
   hipLaunchKernelGGL(decode_combine_kernel, dim3(B, (HQ + 7) / 8), dim3(256),
                      0, st, a);
   return check_launch("decode_combine");
+}
+
+extern "C" int tmopt_attn_decode_paged_noalloc(
+    const void* q, const void* k_pool, const void* v_pool,
+    const int32_t* block_table, int64_t bt_stride, int table_wrap,
+    const int32_t* ctx_lens, int B, int HQ, int HKV, int D, int page_size,
+    int64_t num_pages, int window, float scale, const void* rel,
+    int rel_extent, int min_pages, int num_workgroups, void* out, float* lse,
+    tmopt_stream_t stream) {
+  clear_error();
+  if (B == 0) return TMOPT_OK;
+  // the workspace this launch shape needs (0 for arguments the full entry
+  // point rejects: it reports them)
+  const size_t need =
+      tmopt_attn_decode_workspace_size(B, HQ, HKV, D, num_workgroups);
+  TMOPT_REQUIRE(need <= kScratchBytes, TMOPT_EWORKSPACE,
+                "decode_noalloc: the launch needs %zu bytes of scratch, above "
+                "the %zu-byte static buffer (use tmopt_attn_decode_paged with "
+                "a workspace)",
+                need, kScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != TMOPT_OK) return rc;
+  return tmopt_attn_decode_paged(q, k_pool, v_pool, block_table, bt_stride,
+                                 table_wrap, ctx_lens, B, HQ, HKV, D,
+                                 page_size, num_pages, window, scale, rel,
+                                 rel_extent, min_pages, num_workgroups, out,
+                                 lse, ws, kScratchBytes, stream);
 }

@@ -14,13 +14,19 @@ launch stream (no event between launches: recording one there adds ~7 us
 to a ~100 us decode step).
 
 Secondary lines in "extra": config 3 (window-4096 decode), config 4 (varlen
-prefill, global and window 4096) and the KV-cache write, each with its own
-roofline fraction. The CPU baseline is the fp32 torch oracle on the host
-cores, on a bounded sample of the config-2 batch.
+prefill, global and window 4096), the KV-cache write and config 5 (the
+66-layer mixed step as one hipGraph), each with its own roofline fraction;
+"adapters": the reference-signature entry points at the model's own layer
+shapes with the fused relative bias (attn_global, attn_swa,
+attn_prefill_fused beside the reference's published B300 times). The CPU
+baseline is the fp32 torch oracle on the host cores on the config-2 batch;
+"cpu_baselines" holds configs 3 and 4 and a scaled config-5 estimate, with
+the CPU model.
 
 Prints ONE JSON line.
 """
 import argparse
+import hashlib
 import importlib
 import json
 import os
@@ -238,29 +244,43 @@ def bench_mixed(tm, wl, steps, warmup):
             "seed": st.meta["seed"]}
 
 
+def decode_case_on_host(wl, make):
+    """A decode config generated on the GPU (the same seeded tensors the GPU
+    lines use) and copied to the host: the query, the lengths, and only the
+    pool pages its block table references, with the table renumbered."""
+    c = make(device="cuda", poison=False)
+    t = c.block_table.long()
+    pages = torch.unique(t[t >= 0])
+    remap = torch.full((c.k_pool.shape[0],), -1, dtype=torch.long,
+                       device=t.device)
+    remap[pages] = torch.arange(pages.numel(), device=t.device)
+    table = torch.where(t >= 0, remap[t.clamp(min=0)], t).to(torch.int32)
+    return wl.DecodeCase(c.name, c.q.cpu(), c.k_pool[pages].cpu(),
+                         c.v_pool[pages].cpu(), table.cpu(),
+                         c.ctx_lens.cpu(), c.window, c.scale, c.meta)
+
+
 def cpu_baseline_decode(wl, sample_b=64, reps=5):
     """fp32 torch oracle on the host cores over (by default all 64)
     sequences of config 2; GB/s of algorithmic bytes, median of reps."""
     from oracle import attn_ref
     threads = len(os.sched_getaffinity(0))
     torch.set_num_threads(threads)
-    c = wl.config2(device="cpu", poison=False)
+    c = decode_case_on_host(wl, wl.config2)
     sel = slice(0, sample_b)
     sub = wl.DecodeCase(c.name, c.q[sel], c.k_pool, c.v_pool,
                         c.block_table[sel], c.ctx_lens[sel], c.window,
                         c.scale, c.meta)
-    times = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        attn_ref.decode_paged(sub.q, sub.k_pool, sub.v_pool,
-                              sub.block_table, sub.ctx_lens, sub.scale)
-        times.append(time.perf_counter() - t0)
-    t = sorted(times)[len(times) // 2]
+    t, tot, n = _median_time(
+        lambda: attn_ref.decode_paged(sub.q, sub.k_pool, sub.v_pool,
+                                      sub.block_table, sub.ctx_lens,
+                                      sub.scale), reps, min_total_s=10.0)
     return {"value": sub.algorithmic_bytes() / t / 1e9, "unit": "GB/s",
-            "cores": threads, "kind": "port",
+            "cores": threads, "kind": "port", "cpu_model": cpu_model(),
             "sample": f"config 2, {sample_b} of 64 sequences "
-                      f"({int(sub.ctx_lens.sum())} keys), fp32 torch oracle, "
-                      f"median of {reps} runs ({sum(times):.1f} s total)",
+                      f"({int(sub.ctx_lens.sum())} keys, the GPU line's "
+                      f"inputs), fp32 torch oracle, median of {n} runs "
+                      f"({tot:.1f} s total)",
             "seconds": t}
 
 
@@ -277,15 +297,263 @@ def calibrate_copy():
                       "bytes_written": y.numel() * 2}), flush=True)
 
 
+def source_digest(paths):
+    """sha256 over the given repository files (the kernel sources a profile
+    was taken with), so a run can tell whether a committed profile still
+    describes the code it runs (the GPU box has no git metadata)."""
+    h = hashlib.sha256()
+    for rel in paths:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+DECODE_SOURCES = ("tm-opt_amd/csrc/decode.hip", "tm-opt_amd/csrc/common.h")
+
+
 def measured_traffic():
-    """HBM bytes per decode launch from the committed rocprofv3 PMC summary
-    (profiles/decode_c2_traffic.json), scaled by the copy calibration."""
+    """HBM bytes per C2 decode launch from the committed rocprofv3 PMC
+    summary (profiles/decode_c2_traffic.json: FETCH_SIZE and WRITE_SIZE
+    scaled by a plain copy's counts), with the commit it was recorded at and
+    whether the decode sources are still the ones it was recorded with."""
     path = os.path.join(ROOT, "profiles", "decode_c2_traffic.json")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         t = json.load(f)
-    return int(t["fetch_bytes_per_launch"] + t["write_bytes_per_launch"])
+    return {"bytes": int(t["fetch_bytes_per_launch"] +
+                         t["write_bytes_per_launch"]),
+            "commit": t.get("commit"),
+            "sources_match": t.get("decode_sources_sha256") ==
+            source_digest(DECODE_SOURCES)}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(fn, reps, min_total_s=0.0, max_reps=500):
+    """Median of at least `reps` timed runs, repeated until they add up to
+    min_total_s (a bounded sample of CPU work)."""
+    times = []
+    while len(times) < reps or (sum(times) < min_total_s and
+                                len(times) < max_reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2], sum(times), len(times)
+
+
+def cpu_baselines(wl, reps=3):
+    """fp32 torch oracle on the host cores for configs 3, 4 and 5 (same
+    seeded inputs as the GPU lines; the config-2 headline baseline is
+    cpu_baseline_decode). Config 5: one global and one window layer of the
+    step, timed, then scaled by 16 and 50 layers: an estimate."""
+    from oracle import attn_ref
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    out = {"cores": threads, "cpu_model": cpu_model(), "kind": "port"}
+    c3 = decode_case_on_host(wl, wl.config3)
+    t, tot, n = _median_time(lambda: attn_ref.decode_paged(
+        c3.q, c3.k_pool, c3.v_pool, c3.block_table, c3.ctx_lens, c3.scale,
+        window=c3.window), reps, min_total_s=10.0)
+    out["C3_swa_decode"] = {
+        "value": c3.algorithmic_bytes() / t / 1e9, "unit": "GB/s",
+        "seconds": t, "sample": f"all 128 sequences (the GPU line's "
+                                f"inputs), median of {n} runs "
+                                f"({tot:.1f} s total)"}
+    del c3
+    c4 = wl.config4(window=0, device="cuda")
+    q4, k4, v4, cu4 = c4.q.cpu(), c4.k.cpu(), c4.v.cpu(), c4.cu_seqlens.cpu()
+    t, tot, n = _median_time(lambda: attn_ref.prefill_varlen(
+        q4, k4, v4, cu4, c4.scale), reps, min_total_s=10.0)
+    out["C4_prefill_global"] = {
+        "value": c4.algorithmic_flops() / t / 1e12, "unit": "TFLOP/s",
+        "seconds": t, "sample": f"all 8 runs (the GPU line's inputs), "
+                                f"median of {n} runs ({tot:.1f} s total)"}
+    del c4
+    out["C5_step_estimate"] = cpu_baseline_c5(wl, reps)
+    return out
+
+
+def _layer_to_cpu(st, layer):
+    """CPU copy of one config-5 layer's pages (those its table rows
+    reference), with the table renumbered to them."""
+    kp, vp = st.pool_g if st.is_global[layer] else st.pool_s
+    t = st.tables[layer].long()
+    pages = torch.unique(t)
+    remap = torch.full((kp.shape[0],), -1, dtype=torch.long, device=t.device)
+    remap[pages] = torch.arange(pages.numel(), device=t.device)
+    return kp[pages].cpu(), vp[pages].cpu(), remap[t].cpu()
+
+
+def cpu_baseline_c5(wl, reps):
+    from oracle import attn_ref
+    st = wl.config5(device="cuda")
+    nc = len(st.chunk_lens)
+    q_p, q_d = st.q_prefill.cpu(), st.q_decode.cpu()
+    k_new, v_new = st.k_new.cpu(), st.v_new.cpu()
+    cu_all, start = st.cu_all.cpu().long(), st.start_all.cpu().long()
+    cu_c, prior, ctx = st.cu_chunks.cpu(), st.prior.cpu(), st.dec_ctx.cpu()
+    res = {}
+    for name, layer in (("global", 3), ("swa", 0)):
+        kc, vc, tc = _layer_to_cpu(st, layer)
+        w = 0 if st.is_global[layer] else st.window
+        # per-token flat pool rows of the step's append (the reference's
+        # index_put_ append, kv.py:193-205 / model.py:938-942)
+        rows = torch.repeat_interleave(torch.arange(tc.shape[0]),
+                                       cu_all[1:] - cu_all[:-1])
+        pos = start[rows] + (torch.arange(rows.numel()) - cu_all[rows])
+        flat = tc[rows, pos // 16] * 16 + pos % 16
+        HKV, D = kc.shape[2], kc.shape[3]
+
+        def layer_step():
+            kc.view(-1, HKV, D)[flat] = k_new
+            vc.view(-1, HKV, D)[flat] = v_new
+            attn_ref.prefill_varlen(q_p, None, None, cu_c, st.scale,
+                                    window=w, prior_lens=prior, k_pool=kc,
+                                    v_pool=vc, block_table=tc[:nc])
+            attn_ref.decode_paged(q_d, kc, vc, tc[nc:], ctx, st.scale,
+                                  window=w)
+        t, tot, n = _median_time(layer_step, reps)
+        res[name] = {"seconds_per_layer": t, "total_s": tot, "runs": n}
+        del kc, vc
+    n_g = sum(st.is_global)
+    step = n_g * res["global"]["seconds_per_layer"] + \
+        (st.n_layers - n_g) * res["swa"]["seconds_per_layer"]
+    return {"value": step * 1e3, "unit": "ms per step (estimate)",
+            "per_layer_s": res,
+            "sample": f"one global and one window layer (KV append, chunked "
+                      f"prefill, decode), median of {reps}, scaled by "
+                      f"{n_g} and {st.n_layers - n_g} layers"}
+
+
+def _rel_band_bytes(n, E, HQ):
+    """bf16 bias values a decode row reads: min(visible, E) per head."""
+    return int(torch.clamp(n, max=E).sum()) * HQ * 2
+
+
+def bench_adapters(tm, wl, steps, warmup, n_sets=2):
+    """The reference-signature adapters at the model's own layer shapes, as
+    the engine calls them (model.py:965-976, :522-528): scale 1/D, fused
+    relative bias, the model's head counts. Decode: B=64 with config 2's
+    lengths (attn_global: 64Q/8KV, flat token rows, E=1024; attn_swa: ring
+    W=E=512, 64Q/16KV, full windows). Prefill: the reference's published
+    shape (experiments/ledger.jsonl:29): B=6 padded rows of T=1536, SWA
+    64Q/16KV W=E=512 and global 64Q/8KV E=1024, K/V channel-major as the
+    sconv hands them over."""
+    compat = importlib.import_module("tm-opt_amd.compat")
+    dev = "cuda"
+    bf = torch.bfloat16
+    res = {}
+    g = torch.Generator().manual_seed(wl.SEED0 + 20)
+    D = 128
+    ctx = wl.config2(device="cpu", poison=False).ctx_lens.long()
+    B = ctx.numel()
+
+    # ---- attn_global -------------------------------------------------------
+    HQ, HKV, E = 64, 8, 1024
+    npg = (ctx + 15) // 16
+    width = int(npg.max())
+    P = 2 * int(npg.sum())
+
+    def global_set():
+        kp = torch.randn((P + 1, 16, HKV, D), dtype=bf, device=dev)
+        vp = torch.randn((P + 1, 16, HKV, D), dtype=bf, device=dev)
+        table = torch.randperm(P, generator=g)[:B * width].view(B, width)
+        Lg = int(ctx.max())
+        j = torch.arange(Lg)
+        flat = table[:, j // 16] * 16 + (j % 16)[None]
+        flat = torch.where(j[None] < ctx[:, None], flat,
+                           torch.zeros((), dtype=torch.int64))
+        q = torch.randn((B, HQ, D), dtype=bf, device=dev)
+        rel = torch.randn((B, HQ, E), dtype=bf, device=dev)
+        return (q, kp, vp, flat.to(dev).contiguous(), (ctx - 1).to(dev), rel,
+                Lg)
+    sets = [global_set() for _ in range(n_sets)]
+    wall, ms = time_launches(lambda a: compat.attn_global(*a), sets, steps,
+                             warmup)
+    nbytes = int(ctx.sum()) * HKV * D * 4 + B * HQ * D * 4 + \
+        _rel_band_bytes(ctx, E, HQ) + int(npg.sum()) * 8 + B * 8
+    res["attn_global_b64_64q8kv_e1024"] = {
+        "us_per_call": ms * 1e3, "bytes_per_call": nbytes,
+        "gbs": nbytes / (ms * 1e-3) / 1e9,
+        "roofline_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    # the kernel alone (block table already int32): the adapter's own
+    # helper kernels (table from flat rows, lengths) excluded
+    nat = []
+    for (q, kp, vp, flat, pos, rel, Lg) in sets:
+        nat.append((q, kp, vp, (flat[:, ::16] // 16).to(torch.int32)
+                    .contiguous(), (pos + 1).to(torch.int32), rel,
+                    tm.decode_workspace(B, HQ, HKV, dev),
+                    torch.empty_like(q)))
+    wall, ms = time_launches(lambda a: tm.decode_paged(
+        a[0], a[1], a[2], a[3], a[4], 1.0 / D, rel=a[5], workspace=a[6],
+        out=a[7], return_lse=False), nat, steps, warmup)
+    res["decode_paged_rel_b64_64q8kv_e1024"] = {
+        "us_per_call": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9,
+        "roofline_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    del sets, nat
+
+    # ---- attn_swa ------------------------------------------------------------
+    HQ, HKV, W = 64, 16, 512
+    pos_s = 511 + torch.randint(0, 30000, (B,), generator=g)
+
+    def swa_set():
+        pk = torch.randn((B + 1, W, HKV, D), dtype=bf, device=dev)
+        pv = torch.randn((B + 1, W, HKV, D), dtype=bf, device=dev)
+        slots = torch.randperm(B, generator=g).to(dev)
+        q = torch.randn((B, HQ, D), dtype=bf, device=dev)
+        rel = torch.randn((B, HQ, W), dtype=bf, device=dev)
+        return (q, pk, pv, slots, pos_s.to(dev), rel)
+    sets = [swa_set() for _ in range(n_sets)]
+    wall, ms = time_launches(lambda a: compat.attn_swa(*a), sets, steps,
+                             warmup)
+    nbytes = B * W * HKV * D * 4 + B * HQ * D * 4 + B * HQ * W * 2 + \
+        B * (W // 16) * 4 + B * 16
+    res["attn_swa_b64_64q16kv_w512"] = {
+        "us_per_call": ms * 1e3, "bytes_per_call": nbytes,
+        "gbs": nbytes / (ms * 1e-3) / 1e9,
+        "roofline_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    del sets
+
+    # ---- attn_prefill_fused -----------------------------------------------
+    Bp, T = 6, 1536
+    ref_ms = {"swa": 1.310, "global": 6.156}   # B300, ledger.jsonl:29
+    for kind, HQ, HKV, E, window in (("swa", 64, 16, 512, 512),
+                                     ("global", 64, 8, 1024, None)):
+        def pf_set():
+            q = torch.randn((Bp, T, HQ, D), dtype=bf, device=dev)
+            # channel-major K/V: [B, T, HK*D] with stride 1 along T
+            kc = torch.randn((Bp, HKV * D, T), dtype=bf, device=dev)
+            vc = torch.randn((Bp, HKV * D, T), dtype=bf, device=dev)
+            k = kc.transpose(1, 2).view(Bp, T, HKV, D).transpose(1, 2)
+            v = vc.transpose(1, 2).view(Bp, T, HKV, D).transpose(1, 2)
+            rel = torch.randn((Bp, T, HQ, E), dtype=bf, device=dev)
+            ar = torch.arange(T, device=dev)
+            return (q.transpose(1, 2), k, v, rel.transpose(1, 2), ar, ar,
+                    window)
+        sets = [pf_set() for _ in range(n_sets)]
+        wall, ms = time_launches(lambda a: compat.attn_prefill_fused(*a),
+                                 sets, max(5, steps // 5),
+                                 max(2, warmup // 5))
+        flops = 4 * D * HQ * wl.visible_pairs([T] * Bp, window or 0)
+        res[f"attn_prefill_fused_{kind}_b6_t1536"] = {
+            "ms_per_call": ms, "flops_per_call": flops,
+            "tflops": flops / (ms * 1e-3) / 1e12,
+            "roofline_frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+            "reference_b300_ms": ref_ms[kind],
+            "speedup_vs_reference_b300": ref_ms[kind] / ms,
+            "kv_layout": "channel-major (stride 1 along T)"}
+        del sets
+    return res
 
 
 def main():
@@ -301,6 +569,7 @@ def main():
     ap.add_argument("--wgs", type=int, default=0)
     ap.add_argument("--only", default="")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--cpu-reps", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the paged-"
@@ -348,11 +617,23 @@ def main():
               f"{r['roofline_lower_bound_ms']:.2f} ms)", file=sys.stderr,
               flush=True)
         extra["C5_mixed_step"] = r
+    if args.only in ("", "adapters"):
+        r = bench_adapters(tm, wl, args.steps, args.warmup)
+        for k, x in r.items():
+            print(f"[bench] {k}: " + (f"{x['gbs']:.0f} GB/s" if "gbs" in x
+                                      else f"{x['tflops']:.0f} TFLOP/s"),
+                  file=sys.stderr, flush=True)
+        extra["adapters"] = r
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline_decode(wl)
         print(f"[bench] cpu baseline {cpu['value']:.2f} GB/s on "
               f"{cpu['cores']} threads", file=sys.stderr, flush=True)
+        if args.only == "":
+            extra["cpu_baselines"] = cpu_baselines(wl, args.cpu_reps)
+            print("[bench] cpu baselines C3/C4/C5 done", file=sys.stderr,
+                  flush=True)
+    traffic = measured_traffic()
     line = {
         "metric": _metric(),
         "value": round(head["gbs_wall"], 2),
@@ -371,7 +652,10 @@ def main():
                      "achieved": round(head["gbs_events"], 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["gbs_events"] / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(),
+                     "traffic": traffic and traffic["bytes"],
+                     "traffic_profile_commit": traffic and traffic["commit"],
+                     "traffic_profile_matches_sources":
+                         traffic and traffic["sources_match"],
                      "kernel": "decode_kernel<8,false> + decode_combine_kernel",
                      "bytes_per_launch": head["bytes_per_launch"],
                      "us_per_launch": round(head["us_per_launch_events"], 2)},

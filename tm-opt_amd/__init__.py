@@ -19,7 +19,9 @@ from .attn import (HEAD_DIM, PAGE_SIZE, decode_default_workgroups,
                    decode_paged, decode_paged_noalloc, decode_workspace,
                    decode_workspace_size, kv_write_paged, kv_write_slots,
                    prefill_varlen)
-from .compat import attn_global, attn_prefill_fused, attn_swa
+from .compat import (attn_global, attn_prefill_chunk_global,
+                     attn_prefill_chunk_swa, attn_prefill_fused, attn_swa,
+                     prefill_chunk_state)
 
 __all__ = [
     "TmoptError", "TmoptLibraryMissing", "version", "HEAD_DIM", "PAGE_SIZE",
@@ -27,4 +29,6 @@ __all__ = [
     "decode_workspace",
     "decode_workspace_size", "kv_write_paged", "kv_write_slots",
     "prefill_varlen", "attn_swa", "attn_global", "attn_prefill_fused",
+    "attn_prefill_chunk_swa", "attn_prefill_chunk_global",
+    "prefill_chunk_state",
 ]

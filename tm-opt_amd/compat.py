@@ -127,3 +127,130 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
                         max_seqlen=T, rel=relp, out=out.view(B * T, H, D),
                         return_lse=False, reject=reject)
     return out
+
+
+# --------------------------------------------------------------------------
+# chunked prefill over the engine's KV storage
+# --------------------------------------------------------------------------
+# The reference prefills whole prompts and leaves chunked prefill at
+# Engine.prefill (engine/pyengine/scheduler.py:22-23). These adapters are
+# that seam over its own storage: a chunk's queries attend to the
+# sequence's cached prior context (GlobalPool pages / SwaPool ring rows,
+# kv.py:215-268) plus the chunk's own keys, then the chunk is appended as
+# PagedKV.append / RingKV.append would (kv.py:193-205, :89-103). The prior
+# keys are read in place from the pool (the ring through a ring block
+# table), the chunk's own keys from the packed rows, so the append can come
+# after the attention, which a ring requires (it overwrites positions the
+# chunk's first queries still see).
+
+def _chunk_cu(q, cu_seqlens):
+    if cu_seqlens is None:
+        return torch.tensor([0, q.shape[0]], dtype=torch.int32,
+                            device=q.device)
+    assert cu_seqlens.dtype == torch.int32
+    return cu_seqlens
+
+
+def attn_prefill_chunk_swa(q, k, v, rel, pool_k, pool_v, slots, prior,
+                           cu_seqlens=None, max_seqlen=None):
+    """Chunked prefill of a sliding-window layer over SwaPool ring rows.
+
+    q [total, H, D], k/v [total, HK, D] bf16: the chunks of B sequences
+    packed by cu_seqlens [B+1] int32 (None: one sequence); rel [total, H, W]
+    bf16 or None; pool_k/pool_v [S+1, W, HK, D] (SwaPool; window = W, rel
+    extent = W as attn_swa asserts); slots [B] i64 ring rows; prior [B]
+    i64 tokens each ring has seen (RingKV.n). Scale 1/D. Attends, then
+    appends the chunks to the rings (only the last W positions survive).
+    Returns out [total, H, D] bf16."""
+    total, H, D = q.shape
+    S1, W, HK, _ = pool_k.shape
+    assert pool_k.is_contiguous() and pool_v.is_contiguous()
+    assert pool_v.shape == pool_k.shape and W % PAGE == 0
+    assert slots.dtype == torch.int64 and prior.dtype == torch.int64
+    if rel is not None:
+        assert rel.shape == (total, H, W), (rel.shape, (total, H, W))
+    cu = _chunk_cu(q, cu_seqlens)
+    per = W // PAGE
+    kp = pool_k.view(S1 * per, PAGE, HK, D)
+    vp = pool_v.view(S1 * per, PAGE, HK, D)
+    table = (slots[:, None] * per + torch.arange(
+        per, device=q.device, dtype=torch.int64)[None]).to(torch.int32)
+    start = prior.to(torch.int32)
+    out, _ = attn.prefill_varlen(q, k, v, cu, 1.0 / D, window=W,
+                                 max_seqlen=max_seqlen, prior_lens=start,
+                                 k_pool=kp, v_pool=vp, block_table=table,
+                                 table_wrap=per, rel=rel, return_lse=False)
+    attn.kv_write_paged(k, v, table, start, kp, vp, cu_seqlens=cu,
+                        max_seqlen=max_seqlen, table_wrap=per)
+    return out
+
+
+def attn_prefill_chunk_global(q, k, v, rel, pool_kp, pool_vp, table_dev,
+                              slots, prior, cu_seqlens=None,
+                              max_seqlen=None):
+    """Chunked prefill of a global layer over GlobalPool pages.
+
+    q [total, H, D], k/v [total, HK, D] bf16 packed by cu_seqlens [B+1]
+    int32 (None: one sequence); rel [total, H, E] bf16 or None;
+    pool_kp/pool_vp [(P+1), 16, HK, D]; table_dev [S+1, num_pages] i64
+    (GlobalPool's device page table, already covering each sequence's
+    prior + chunk positions: PagedKV.ensure_pages, kv.py:170-191); slots
+    [B] i64; prior [B] i64 (PagedKV.n). Scale 1/D, causal. Attends, then
+    appends the chunks through the page table. Returns out [total, H, D]."""
+    total, H, D = q.shape
+    assert pool_kp.is_contiguous() and pool_vp.is_contiguous()
+    assert pool_kp.shape[1] == PAGE
+    assert table_dev.dtype == torch.int64 and table_dev.dim() == 2
+    assert slots.dtype == torch.int64 and prior.dtype == torch.int64
+    if rel is not None:
+        assert rel.shape[:2] == (total, H)
+    cu = _chunk_cu(q, cu_seqlens)
+    table = table_dev[slots].to(torch.int32)
+    start = prior.to(torch.int32)
+    out, _ = attn.prefill_varlen(q, k, v, cu, 1.0 / D, window=0,
+                                 max_seqlen=max_seqlen, prior_lens=start,
+                                 k_pool=pool_kp, v_pool=pool_vp,
+                                 block_table=table, rel=rel,
+                                 return_lse=False)
+    attn.kv_write_paged(k, v, table, start, pool_kp, pool_vp, cu_seqlens=cu,
+                        max_seqlen=max_seqlen)
+    return out
+
+
+def prefill_chunk_state(q, k, v, rel, cache):
+    """One sequence's chunk against its own cache object, shaped like the
+    reference's PagedKV (kp, vp [P, 16, HK, D], table_dev_row [num_pages]
+    i64, n, page_size, ensure_pages(last_page)) or RingKV (k, v [W, HK, D],
+    n): the cache's pages are allocated for the chunk on the host as
+    PagedKV.append does (kv.py:196-198), the chunk attends to the n cached
+    tokens plus itself (window = W on a ring, causal on pages; scale 1/D)
+    and is appended, and cache.n advances by the chunk length.
+    q [T, H, D], k/v [T, HK, D] bf16, rel [T, H, E] or None.
+    Returns out [T, H, D] bf16."""
+    T, H, D = q.shape
+    dev = q.device
+    n = int(cache.n)
+    prior = torch.tensor([n], dtype=torch.int32, device=dev)
+    cu = torch.tensor([0, T], dtype=torch.int32, device=dev)
+    if hasattr(cache, "table_dev_row"):
+        ps = cache.page_size
+        assert ps == PAGE and cache.table_dev_row is not None
+        cache.ensure_pages((n + T - 1) // ps)
+        table = cache.table_dev_row.to(torch.int32)[None].contiguous()
+        kp, vp, wrap, window = cache.kp, cache.vp, 0, 0
+    else:
+        W = cache.k.shape[0]
+        assert W % PAGE == 0 and cache.k.is_contiguous()
+        per = W // PAGE
+        kp = cache.k.view(per, PAGE, *cache.k.shape[1:])
+        vp = cache.v.view(per, PAGE, *cache.v.shape[1:])
+        table = torch.arange(per, dtype=torch.int32, device=dev)[None]
+        wrap, window = per, W
+    out, _ = attn.prefill_varlen(q, k, v, cu, 1.0 / D, window=window,
+                                 max_seqlen=T, prior_lens=prior, k_pool=kp,
+                                 v_pool=vp, block_table=table,
+                                 table_wrap=wrap, rel=rel, return_lse=False)
+    attn.kv_write_paged(k, v, table, prior, kp, vp, cu_seqlens=cu,
+                        max_seqlen=T, table_wrap=wrap)
+    cache.n = n + T
+    return out

@@ -209,3 +209,131 @@ class MixedStepGraph:
 
     def replay(self):
         self.graph.replay()
+
+
+BUCKET = 512   # the reference's padded-key-length bucket (graphrun.py)
+
+
+class AttnGraphRunner:
+    """The attention part of the reference's graphed decode step, captured
+    with GraphRunner's semantics (engine/pyengine/graphrun.py:76-380) around
+    the reference-signature adapters (compat.attn_global / attn_swa):
+
+      * static row buffers padded to max_batch: the host stages the live
+        rows' positions and slots, dead rows get position 0 and the scratch
+        slot max_batch (SwaPool's scratch row, GlobalPool's scratch page
+        behind table_dev[max_batch], kv.py:223-228, :262-268);
+      * per layer, the step's own index math as model.py:926-950 computes
+        it (page gather of the new token's flat row, ring slot pos % W), the
+        append (tmopt_kv_write_slots, the index_put_ of model.py:941-948),
+        the padded per-token flat rows of the global gather at the bucket
+        length L_pad (decode_batch_ctx_static, model.py:860-887) and the
+        attention call (model.py:970-976);
+      * one captured program per L_pad = ceil((max pos + 1) / 512) * 512,
+        a monotone high-water mark capped at the table's reach, captured
+        on first sight after two warm-ups under the dead-row config (so
+        warm-ups touch only scratch state) and replayed for every step of
+        that bucket (graphrun.py:260-301, :338-361).
+
+    layers: dicts with kind "global" (kp, vp [(P+1), 16, HK, D], table_dev
+    [max_batch+1, num_pages] i64) or "swa" (k, v [max_batch+1, W, HK, D]).
+    Before step(): fill q[l] [MB, HQ, D], k_new[l] / v_new[l] [MB, HK, D],
+    rel[l] [MB, HQ, E] for the live rows (dead rows are don't-care).
+    After step(): out[l] [MB, HQ, D] (dead rows are don't-care)."""
+
+    def __init__(self, layers, max_batch, HQ, D=attn.HEAD_DIM,
+                 device="cuda"):
+        self.layers = layers
+        self.MB = max_batch
+        self.scratch = max_batch
+        dev = torch.device(device)
+        self.device = dev
+        bf = torch.bfloat16
+        self.pos_buf = torch.zeros(max_batch, dtype=torch.int64, device=dev)
+        self.slots_buf = torch.full((max_batch,), self.scratch,
+                                    dtype=torch.int64, device=dev)
+        self.q, self.k_new, self.v_new, self.rel, self.out = [], [], [], [], []
+        reach = None
+        for ly in layers:
+            if ly["kind"] == "global":
+                HK = ly["kp"].shape[2]
+                E = ly.get("rel_extent", 1024)
+                r = ly["table_dev"].shape[1] * ly["kp"].shape[1]
+                reach = r if reach is None else min(reach, r)
+            else:
+                HK = ly["k"].shape[2]
+                E = ly["k"].shape[1]
+            self.q.append(torch.zeros((max_batch, HQ, D), dtype=bf,
+                                      device=dev))
+            self.k_new.append(torch.zeros((max_batch, HK, D), dtype=bf,
+                                          device=dev))
+            self.v_new.append(torch.zeros((max_batch, HK, D), dtype=bf,
+                                          device=dev))
+            self.rel.append(torch.zeros((max_batch, HQ, E), dtype=bf,
+                                        device=dev))
+            self.out.append(torch.zeros((max_batch, HQ, D), dtype=bf,
+                                        device=dev))
+        self.reach = reach
+        self.programs = {}
+        self.hiwater = 0
+        self.captures = 0
+
+    def _run(self, L_pad):
+        from . import compat
+        pos, slots = self.pos_buf, self.slots_buf
+        n = pos + 1
+        for l, ly in enumerate(self.layers):
+            q, k, v, rel = self.q[l], self.k_new[l], self.v_new[l], self.rel[l]
+            if ly["kind"] == "global":
+                kp, vp, td = ly["kp"], ly["vp"], ly["table_dev"]
+                ps = kp.shape[1]
+                HK, D = kp.shape[2], kp.shape[3]
+                table = td[slots]                              # [MB, pages]
+                flat_new = (table.gather(1, (pos // ps)[:, None])[:, 0] * ps
+                            + pos % ps)
+                attn.kv_write_slots(k, v, flat_new, kp.view(-1, HK, D),
+                                    vp.view(-1, HK, D))
+                j = torch.arange(L_pad, device=pos.device)
+                flat = table[:, j // ps] * ps + (j % ps)[None, :]
+                flat = flat.masked_fill(j[None, :] >= n[:, None], 0)
+                self.out[l].copy_(compat.attn_global(q, kp, vp, flat, pos,
+                                                     rel, L_pad))
+            else:
+                pk, pv = ly["k"], ly["v"]
+                W, HK, D = pk.shape[1], pk.shape[2], pk.shape[3]
+                rows = slots * W + pos % W                     # ring slot
+                attn.kv_write_slots(k, v, rows, pk.view(-1, HK, D),
+                                    pv.view(-1, HK, D))
+                self.out[l].copy_(compat.attn_swa(q, pk, pv, slots, pos,
+                                                  rel))
+
+    def _capture(self, L_pad):
+        # dead-row config in every static input: the executed warm-ups only
+        # write the scratch slot / page (graphrun.py:267-277)
+        self.pos_buf.zero_()
+        self.slots_buf.fill_(self.scratch)
+        g = StepGraph(lambda: self._run(L_pad), self.device).capture()
+        self.programs[L_pad] = g
+        self.captures += 1
+
+    def bucket(self, pos):
+        L = -(-(max(pos) + 1) // BUCKET) * BUCKET
+        L = max(L, self.hiwater)
+        return min(L, self.reach) if self.reach is not None else L
+
+    def step(self, pos, slots):
+        """One graphed step for the live rows: pos / slots host int lists in
+        row order (len <= max_batch). Returns the L_pad bucket replayed."""
+        B = len(pos)
+        assert B == len(slots) and 0 < B <= self.MB
+        L_pad = self.bucket(pos)
+        if L_pad not in self.programs:
+            self._capture(L_pad)
+        self.hiwater = L_pad
+        dead = self.MB - B
+        self.pos_buf.copy_(torch.tensor(list(pos) + [0] * dead,
+                                        dtype=torch.int64))
+        self.slots_buf.copy_(torch.tensor(list(slots) + [self.scratch] * dead,
+                                          dtype=torch.int64))
+        self.programs[L_pad].replay()
+        return L_pad

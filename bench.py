@@ -440,6 +440,79 @@ def _rel_band_bytes(n, E, HQ):
     return int(torch.clamp(n, max=E).sum()) * HQ * 2
 
 
+class _BenchPages:
+    """A pool-backed page cache shaped like the reference's PagedKV
+    (kv.py:117-212), fresh for every timed call (a whole-prompt prefill)."""
+
+    def __init__(self, kp, vp, free, row):
+        self.kp, self.vp, self.free, self.table_dev_row = kp, vp, free, row
+        self.page_size, self.table, self.n = 16, [], 0
+
+    def ensure_pages(self, last):
+        first = len(self.table)
+        while len(self.table) <= last:
+            self.table.append(self.free.pop())
+        self.table_dev_row[first:len(self.table)] = torch.tensor(
+            self.table[first:], device=self.table_dev_row.device)
+
+
+class _BenchRing:
+    def __init__(self, k, v):
+        self.k, self.v, self.n = k, v, 0
+
+
+def bench_prefill_append(tm, compat, sets, window, HKV, steps, warmup):
+    """One prefill layer's cache population + attention, as the engine runs
+    it (model.py:507-528), two ways: (a) the append of every row from the
+    sconv's channel-major K/V (tmopt_kv_write_paged reads them in place)
+    followed by attn_prefill_fused (packed copy of K/V + kernel); (b)
+    attn_prefill_fused given the caches (append inside; a global layer then
+    reads its keys from the pages: no copy). a - b is the copy removed."""
+    q0, k0 = sets[0][0], sets[0][1]
+    Bp, H, T, D = q0.shape
+    npg = (T + 15) // 16
+    P = Bp * npg
+    dev = q0.device
+    pools = [(torch.empty((P, 16, HKV, D), dtype=torch.bfloat16, device=dev),
+              torch.empty((P, 16, HKV, D), dtype=torch.bfloat16, device=dev))
+             for _ in sets]
+    rows = [torch.zeros(npg, dtype=torch.int64, device=dev)
+            for _ in range(Bp)]
+    W = window or 0
+    rings = [[(torch.empty((W, HKV, D), dtype=torch.bfloat16, device=dev),
+               torch.empty((W, HKV, D), dtype=torch.bfloat16, device=dev))
+              for _ in range(Bp)] for _ in sets] if window else None
+
+    def caches(si):
+        if window:
+            return [_BenchRing(*r) for r in rings[si]]
+        free = list(range(P))
+        return [_BenchPages(pools[si][0], pools[si][1], free, rows[b])
+                for b in range(Bp)]
+
+    order = {id(s): i for i, s in enumerate(sets)}
+
+    def separate(a):
+        cs = caches(order[id(a)])
+        compat._append_rows(a[1], a[2], cs, [T] * Bp)
+        compat.attn_prefill_fused(*a)
+
+    def fused(a):
+        compat.attn_prefill_fused(*a, caches=caches(order[id(a)]))
+
+    _, ms_a = time_launches(separate, sets, max(5, steps // 5),
+                            max(2, warmup // 5))
+    _, ms_b = time_launches(fused, sets, max(5, steps // 5),
+                            max(2, warmup // 5))
+    kv_bytes = 2 * Bp * HKV * T * D * 2
+    return {"ms_append_then_attention": ms_a,
+            "ms_attention_with_caches": ms_b,
+            "ms_removed": ms_a - ms_b,
+            "kv_copy_bytes_avoidable": kv_bytes * 2,
+            "note": "global: keys read back from the pages just written; "
+                    "SWA rings cannot hold T > W, so the packed copy stays"}
+
+
 def bench_adapters(tm, wl, steps, warmup, n_sets=2):
     """The reference-signature adapters at the model's own layer shapes, as
     the engine calls them (model.py:965-976, :522-528): scale 1/D, fused
@@ -552,6 +625,9 @@ def bench_adapters(tm, wl, steps, warmup, n_sets=2):
             "reference_b300_ms": ref_ms[kind],
             "speedup_vs_reference_b300": ref_ms[kind] / ms,
             "kv_layout": "channel-major (stride 1 along T)"}
+        res[f"prefill_layer_{kind}_b6_t1536_with_append"] = \
+            bench_prefill_append(tm, compat, sets, window, HKV, steps,
+                                 warmup)
         del sets
     return res
 
@@ -620,9 +696,14 @@ def main():
     if args.only in ("", "adapters"):
         r = bench_adapters(tm, wl, args.steps, args.warmup)
         for k, x in r.items():
-            print(f"[bench] {k}: " + (f"{x['gbs']:.0f} GB/s" if "gbs" in x
-                                      else f"{x['tflops']:.0f} TFLOP/s"),
-                  file=sys.stderr, flush=True)
+            if "gbs" in x:
+                txt = f"{x['gbs']:.0f} GB/s"
+            elif "tflops" in x:
+                txt = f"{x['tflops']:.0f} TFLOP/s"
+            else:
+                txt = (f"{x['ms_append_then_attention']:.3f} ms -> "
+                       f"{x['ms_attention_with_caches']:.3f} ms")
+            print(f"[bench] {k}: {txt}", file=sys.stderr, flush=True)
         extra["adapters"] = r
     cpu = None
     if not args.no_cpu:

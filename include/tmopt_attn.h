@@ -97,10 +97,19 @@ int tmopt_kv_write_slots(const void* k, const void* v, int64_t k_stride_tok,
  * Table entries outside [0, num_pages) are skipped, never dereferenced,
  * and so are tokens whose logical page lies past the row width (index >=
  * bt_stride).
+ * Element strides: k[row, h, d] = k + row * k_stride_tok + h * k_stride_head
+ * + d * k_stride_dim (v likewise). k_stride_dim == 1 (token-major rows,
+ * 16-byte aligned) is the general form. Channel-major K / V -- tokens
+ * contiguous (k_stride_tok == 1), head_dim strided, as the sconv hands the
+ * prefill's K / V to the cache append (engine/pyengine/model.py:486-512,
+ * experiments/DEADENDS.md:631-645) -- are read in place and transposed on
+ * chip: D == 128, k_stride_dim, k_stride_head multiples of 8, 16-byte
+ * aligned base (TMOPT_EUNSUPPORTED otherwise).
  */
 int tmopt_kv_write_paged(const void* k, const void* v, int64_t k_stride_tok,
-                         int64_t k_stride_head, int64_t v_stride_tok,
-                         int64_t v_stride_head, const int32_t* cu_seqlens,
+                         int64_t k_stride_head, int64_t k_stride_dim,
+                         int64_t v_stride_tok, int64_t v_stride_head,
+                         int64_t v_stride_dim, const int32_t* cu_seqlens,
                          const int32_t* start_pos, int num_seqs, int max_seqlen,
                          const int32_t* block_table, int64_t bt_stride,
                          int table_wrap, int page_size, int HKV, int D,

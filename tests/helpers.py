@@ -30,3 +30,34 @@ def assert_lse_close(got, ref, what=""):
     m = float(err.max()) if err.numel() else 0.0
     assert m <= LSE_ATOL, f"{what}: LSE max err {m:.3g} > {LSE_ATOL}"
     return m
+
+
+class PagedCache:
+    """Shaped like the reference's pool-backed PagedKV (kv.py:117-212):
+    shared pools, a host page list filled from a free list on demand and
+    mirrored into a device table row, n tokens stored."""
+
+    def __init__(self, kp, vp, free, table_dev_row):
+        self.kp, self.vp = kp, vp
+        self.free = free
+        self.table_dev_row = table_dev_row
+        self.page_size = 16
+        self.table = []
+        self.n = 0
+
+    def ensure_pages(self, last_page):
+        first = len(self.table)
+        while len(self.table) <= last_page:
+            self.table.append(self.free.pop(0))
+        if len(self.table) > first:
+            self.table_dev_row[first:len(self.table)] = torch.tensor(
+                self.table[first:], device=self.table_dev_row.device)
+
+
+class RingCache:
+    """Shaped like the reference's RingKV (kv.py:66-114): a [W, HK, D] ring
+    per K and V, position p at slot p % W, n tokens seen."""
+
+    def __init__(self, k, v):
+        self.k, self.v = k, v
+        self.n = 0

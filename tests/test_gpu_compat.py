@@ -121,3 +121,60 @@ def test_attn_prefill_fused_positions(tm, dev):
         assert torch.isnan(out.float()).all()
     with pytest.raises(AssertionError):
         tm.attn_prefill_fused(q, k, v, rel, bad_q.cpu(), ar.cpu(), E)
+
+
+@pytest.mark.parametrize("kind", ["global", "swa"])
+def test_attn_prefill_fused_populates_caches(tm, dev, kind):
+    """attn_prefill_fused given the rows' caches (the engine's
+    st.cache.append(kn[i, :lens[i]], vv[i, :lens[i]]) at model.py:507-512)
+    appends the channel-major K/V itself; a global layer then reads its keys
+    back from the pages (no packed copy), an SWA layer keeps the packed
+    source and fills its rings. The live rows equal the packed path's
+    bitwise, every cache holds its row's tokens bit-exact, n advances."""
+    import numpy as np
+    from helpers import PagedCache, RingCache
+    from oracle import kv_ref
+    g = torch.Generator().manual_seed(17)
+    B, T, D = 3, 200, 128
+    lens = [200, 150, 77]
+    if kind == "global":
+        hq, hk, E, window = 64, 8, 1024, None
+    else:
+        hq, hk, E, window = 64, 16, 512, 512
+    bf = torch.bfloat16
+    q = torch.randn((B, T, hq, D), generator=g).to(bf).to(dev).transpose(1, 2)
+    kc = torch.randn((B, hk * D, T), generator=g).to(bf).to(dev)
+    vc = torch.randn((B, hk * D, T), generator=g).to(bf).to(dev)
+    k = kc.transpose(1, 2).view(B, T, hk, D).transpose(1, 2)   # sconv layout
+    v = vc.transpose(1, 2).view(B, T, hk, D).transpose(1, 2)
+    rel = (torch.randn((B, T, hq, E), generator=g) * 0.5).to(bf).to(
+        dev).transpose(1, 2)
+    ar = torch.arange(T, device=dev)
+    base = tm.attn_prefill_fused(q, k, v, rel, ar, ar, window)
+    if kind == "global":
+        P = 64
+        free = torch.randperm(P, generator=g).tolist()
+        kp = torch.zeros((P, 16, hk, D), dtype=bf, device=dev)
+        vp = torch.zeros_like(kp)
+        caches = [PagedCache(kp, vp, free, torch.zeros(
+            P // 2, dtype=torch.int64, device=dev)) for _ in range(B)]
+    else:
+        caches = [RingCache(torch.zeros((E, hk, D), dtype=bf, device=dev),
+                            torch.zeros((E, hk, D), dtype=bf, device=dev))
+                  for _ in range(B)]
+    out = tm.attn_prefill_fused(q, k, v, rel, ar, ar, window, caches=caches,
+                                lens=lens)
+    torch.cuda.synchronize()
+    for i, n in enumerate(lens):
+        assert torch.equal(out[i, :n], base[i, :n]), f"row {i}"
+        c = caches[i]
+        assert c.n == n
+        rows = k[i].transpose(0, 1)[:n].contiguous()             # [n, hk, D]
+        if kind == "global":
+            got = kv_ref.gather(kv_ref.as_u16(c.kp), c.table, n)
+        else:
+            got = kv_ref.gather(kv_ref.as_u16(c.k).reshape(E // 16, 16, hk, D),
+                                list(range(E // 16)), n,
+                                table_wrap=E // 16, lo=max(0, n - E))
+            rows = rows[max(0, n - E):]
+        assert np.array_equal(got, kv_ref.as_u16(rows)), f"cache row {i}"

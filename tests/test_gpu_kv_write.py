@@ -325,3 +325,97 @@ def test_write_paged_row_width_bound(tm, dev):
     # positions 32..39 (logical page 2) were skipped: pages 5 and 12 intact
     assert torch.equal(kd[5].cpu(), kp[5]) and torch.equal(kd[12].cpu(),
                                                           kp[12])
+
+
+def _channel_major(rows, T_pad=None):
+    """A [T, H, D] tensor with the same values laid out channel-major:
+    tokens contiguous, head_dim strided (T_pad >= T tokens per dim row)."""
+    T, H, D = rows.shape
+    T_pad = T_pad or T
+    buf = torch.zeros((H, D, T_pad), dtype=rows.dtype, device=rows.device)
+    buf[:, :, :T] = rows.permute(1, 2, 0)
+    return buf.permute(2, 0, 1)[:T]            # [T, H, D], strides (1, D*Tp, Tp)
+
+
+@pytest.mark.parametrize("wrap", [0, 5])
+def test_write_paged_channel_major_packed(tm, dev, wrap):
+    """Channel-major K/V (tokens contiguous, head_dim strided) read in place:
+    runs starting off the 8-token grid, a run ending at the tensor's last
+    row, a ring table with RingKV's drop rule; bit-exact against the
+    token-major rows' append."""
+    g = torch.Generator().manual_seed(55 + wrap)
+    H, D = 4, 128
+    lens = [5, 133, 64, 1, 70, 199]           # 472 tokens: a multiple of 8
+    start = [0, 7, 100, 3, 20, 61]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    T = int(cu[-1])
+    k = _bf16((T, H, D), g)
+    v = _bf16((T, H, D), g)
+    per = [wrap if wrap else (s + n + 15) // 16 for s, n in zip(start, lens)]
+    width = max(per)
+    P = sum(per) + 2
+    perm = torch.randperm(P, generator=g).to(torch.int32)
+    table = torch.full((len(lens), width), -1, dtype=torch.int32)
+    off = 0
+    for i, n in enumerate(per):
+        table[i, :n] = perm[off:off + n]
+        off += n
+    kp = _bf16((P, 16, H, D), g)
+    vp = _bf16((P, 16, H, D), g)
+    want_k = kv_ref.write_paged(kv_ref.as_u16(kp).copy(), kv_ref.as_u16(k),
+                                cu, start, table.numpy(), 16, wrap)
+    want_v = kv_ref.write_paged(kv_ref.as_u16(vp).copy(), kv_ref.as_u16(v),
+                                cu, start, table.numpy(), 16, wrap)
+    # K tight (the last run ends at the tensor's last element), V with dim
+    # rows padded past the tokens
+    kc = _channel_major(k.to(dev))
+    vc = _channel_major(v.to(dev), T_pad=T + 24)
+    assert kc.stride() == (1, D * T, T) and vc.stride(0) == 1
+    kd, vd = kp.to(dev), vp.to(dev)
+    tm.kv_write_paged(kc, vc, table.to(dev),
+                      torch.tensor(start, dtype=torch.int32, device=dev), kd,
+                      vd, cu_seqlens=torch.from_numpy(cu).to(dev),
+                      table_wrap=wrap)
+    torch.cuda.synchronize()
+    assert np.array_equal(kv_ref.as_u16(kd), want_k)
+    assert np.array_equal(kv_ref.as_u16(vd), want_v)
+
+
+def test_write_paged_channel_major_engine_views(tm, dev):
+    """The reference prefill's own append (model.py:507-512): the sconv
+    hands K/V over channel-major, [B, T, C] with stride 1 along T, viewed
+    as [B, T, HK, D]; each sequence appends kn[i, :len_i] (a strided view)
+    through its own table. Every call reads the view in place."""
+    g = torch.Generator().manual_seed(57)
+    B, T, HK, D = 3, 96, 8, 128
+    lens = [96, 37, 1]
+    C = HK * D
+    kc = _bf16((B, C, T), g)                   # channel-major storage
+    vc = _bf16((B, C, T), g)
+    kn = kc.transpose(1, 2).view(B, T, HK, D)  # strides (C*T, 1, D*T, T)
+    vn = vc.transpose(1, 2).view(B, T, HK, D)
+    P = 40
+    perm = torch.randperm(P, generator=g).to(torch.int32)
+    tables = perm[:B * 8].view(B, 8)
+    kp = _bf16((P, 16, HK, D), g)
+    vp = _bf16((P, 16, HK, D), g)
+    want_k = kv_ref.as_u16(kp).copy()
+    want_v = kv_ref.as_u16(vp).copy()
+    kd, vd = kp.to(dev), vp.to(dev)
+    knd = kc.to(dev).transpose(1, 2).view(B, T, HK, D)
+    vnd = vc.to(dev).transpose(1, 2).view(B, T, HK, D)
+    for i, n in enumerate(lens):
+        kv_ref.write_paged(want_k, kv_ref.as_u16(kn[i, :n].contiguous()),
+                           [0, n], [0], tables[i:i + 1].numpy())
+        kv_ref.write_paged(want_v, kv_ref.as_u16(vn[i, :n].contiguous()),
+                           [0, n], [0], tables[i:i + 1].numpy())
+        assert knd[i, :n].stride() == (1, D * T, T)
+        tm.kv_write_paged(knd[i, :n], vnd[i, :n],
+                          tables[i:i + 1].to(dev).contiguous(),
+                          torch.zeros(1, dtype=torch.int32, device=dev), kd,
+                          vd, cu_seqlens=torch.tensor([0, n],
+                                                      dtype=torch.int32,
+                                                      device=dev))
+    torch.cuda.synchronize()
+    assert np.array_equal(kv_ref.as_u16(kd), want_k)
+    assert np.array_equal(kv_ref.as_u16(vd), want_v)

@@ -45,7 +45,8 @@ SIGNATURES = {
         _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_i64,
         _c_i32, _c_i32, _c_ptr, _c_ptr, _c_i64, _c_ptr]),
     "tmopt_kv_write_paged": (_c_i32, [
-        _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_ptr, _c_ptr,
+        _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+        _c_ptr, _c_ptr,
         _c_i32, _c_i32, _c_ptr, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,
         _c_ptr, _c_ptr, _c_i64, _c_ptr]),
     "tmopt_attn_decode_default_workgroups": (_c_i32, [_c_i32]),

@@ -54,19 +54,30 @@ def kv_write_slots(k, v, slot_mapping, k_pool, v_pool):
               HKV, D, _ptr(k_pool), _ptr(v_pool), rows, _stream(dev))
 
 
+def _channel_major(x):
+    """Rows [T, H, D] with contiguous tokens and a strided head_dim (the
+    sconv output's layout) rather than contiguous head_dim rows."""
+    return x.stride(-1) != 1 and x.stride(0) == 1
+
+
 def kv_write_paged(k, v, block_table, start_pos, k_pool, v_pool,
                    cu_seqlens=None, max_seqlen=None, table_wrap=0):
     """Append token runs through a block table (positions computed in-kernel).
 
-    k, v [T, HKV, D]; block_table [S, bt_stride] int32; start_pos [S] int32;
+    k, v [T, HKV, D] bf16: token-major rows (head_dim contiguous) or
+    channel-major ones (tokens contiguous, head_dim strided: the sconv
+    output the reference's prefill appends, model.py:486-512), read in place
+    either way; block_table [S, bt_stride] int32; start_pos [S] int32;
     cu_seqlens [S+1] int32 or None (one token per sequence: the decode
     step); pools [num_pages, page_size, HKV, D]. table_wrap > 0 makes each
     table row a ring of table_wrap pages (sliding-window pools).
     Reference: engine/pyengine/kv.py:89-103, :193-205; model.py:938-948."""
     T, HKV, D = k.shape
     assert v.shape == k.shape
-    _check_rows(k, "k")
-    _check_rows(v, "v")
+    for x, name in ((k, "k"), (v, "v")):
+        assert x.dtype == torch.bfloat16, f"{name} must be bf16"
+        assert x.stride(-1) == 1 or _channel_major(x), \
+            f"{name}: head_dim or tokens must be contiguous"
     assert block_table.dtype == torch.int32 and block_table.dim() == 2
     assert block_table.stride(1) == 1
     assert start_pos.dtype == torch.int32
@@ -87,7 +98,8 @@ def kv_write_paged(k, v, block_table, start_pos, k_pool, v_pool,
     P, page_size = k_pool.shape[0], k_pool.shape[1]
     assert tuple(k_pool.shape[2:]) == (HKV, D)
     _lib.call("tmopt_kv_write_paged", _ptr(k), _ptr(v), k.stride(0),
-              k.stride(1), v.stride(0), v.stride(1), _ptr(cu_seqlens),
+              k.stride(1), k.stride(2), v.stride(0), v.stride(1),
+              v.stride(2), _ptr(cu_seqlens),
               _ptr(start_pos), S, int(max_seqlen), _ptr(block_table),
               block_table.stride(0), int(table_wrap), page_size, HKV, D,
               _ptr(k_pool), _ptr(v_pool), P, _stream(k.device))

@@ -80,14 +80,69 @@ def _packed(x, B, T, H, D):
     return xt.as_strided((B * T, H, D), (xt.stride(1), xt.stride(2), 1))
 
 
+def _append_rows(k, v, caches, lens):
+    """The prefill's cache population (model.py:507-512:
+    st.cache.append(kn[i, :lens[i]], vv[i, :lens[i]])) done natively: each
+    row's K/V [lens[i], HK, D] is appended to its cache straight from the
+    (channel-major or token-major) views, pages allocated on the host as
+    PagedKV.append does (kv.py:196-198), ring rows as RingKV.append keeps
+    them (kv.py:89-103); cache.n advances. Returns the int32 block-table
+    rows of page caches ([B, num_pages]) or None for rings."""
+    B = k.shape[0]
+    dev = k.device
+    rows = []
+    # every row's start position and run bounds in one host-to-device copy
+    # (a copy from pageable memory synchronises the stream)
+    meta = torch.tensor([[int(caches[i].n), 0, int(lens[i])]
+                         for i in range(B)], dtype=torch.int32).to(dev)
+    for i in range(B):
+        c = caches[i]
+        n0, T = int(c.n), int(lens[i])
+        kt = k[i].transpose(0, 1)[:T]            # [T, HK, D] view
+        vt = v[i].transpose(0, 1)[:T]
+        start, cu = meta[i, 0:1], meta[i, 1:3]
+        if hasattr(c, "kp"):
+            c.ensure_pages((n0 + T - 1) // c.page_size)
+            if getattr(c, "table_dev_row", None) is not None:
+                row = c.table_dev_row.to(torch.int32)[None]
+            else:                                # a PagedKV with its own pool
+                row = torch.tensor([c.table], dtype=torch.int32, device=dev)
+            attn.kv_write_paged(kt, vt, row, start, c.kp, c.vp,
+                                cu_seqlens=cu, max_seqlen=T)
+            rows.append(row)
+        else:
+            W = c.k.shape[0]
+            per = W // PAGE
+            ring = torch.arange(per, dtype=torch.int32, device=dev)[None]
+            attn.kv_write_paged(kt, vt, ring, start,
+                                c.k.view(per, PAGE, *c.k.shape[1:]),
+                                c.v.view(per, PAGE, *c.v.shape[1:]),
+                                cu_seqlens=cu, max_seqlen=T, table_wrap=per)
+        c.n = n0 + T
+    if not rows:
+        return None
+    width = max(r.shape[1] for r in rows)
+    return torch.cat([torch.nn.functional.pad(r, (0, width - r.shape[1]),
+                                              value=-1) for r in rows])
+
+
 def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
-                       block_m=64, block_n=64):
+                       block_m=64, block_n=64, caches=None, lens=None):
     """Fused prefill attention over in-batch K/V (attn_prefill.py:144).
     q [B, H, T, D], k/v [B, HK, T, D] bf16 (any strides), rel [B, H, T, E]
     bf16 with rel.stride(3) == 1, q_positions/kv_positions [T] i64 (the
     engine's arange), window None (global) or W (SWA, E == W).
     Returns [B, T, H, D] bf16. block_m / block_n are accepted for signature
-    compatibility; the kernel's tiles are fixed for gfx950."""
+    compatibility; the kernel's tiles are fixed for gfx950.
+
+    caches / lens (optional, not in the reference signature): the B rows'
+    cache objects (PagedKV- or RingKV-shaped, empty: a whole-prompt
+    prefill) and live lengths (default T) whose population the engine does
+    just before this call (model.py:507-512). The adapter then appends the
+    rows itself, reading the sconv's channel-major K/V in place, and a
+    global layer's attention reads its keys back from those pages: the
+    packed copy of K/V is gone. Rings (SWA) cannot hold a prompt longer
+    than the window, so their attention keeps the packed source."""
     B, H, T, D = q.shape
     HK = k.shape[1]
     E = rel.shape[3]
@@ -114,17 +169,36 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
             "q_positions and kv_positions must be the same p0 + arange(T)"
     reject = bad.to(device=dev, dtype=torch.int32).reshape(1)
     qp = _packed(q, B, T, H, D)
-    kp = _packed(k, B, T, HK, D)
-    vp = _packed(v, B, T, HK, D)
     rt = rel.transpose(1, 2)                     # [B, T, H, E]
     if not (B == 1 or rt.stride(0) == T * rt.stride(1)):
         rt = rt.contiguous()
     relp = rt.as_strided((B * T, H, E), (rt.stride(1), rt.stride(2), 1))
     out = torch.empty((B, T, H, D), dtype=q.dtype, device=dev)
     cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=dev)
-    attn.prefill_varlen(qp, kp, vp, cu, 1.0 / D,
-                        window=0 if window is None else int(window),
-                        max_seqlen=T, rel=relp, out=out.view(B * T, H, D),
+    w = 0 if window is None else int(window)
+    table = None
+    if caches is not None:
+        assert len(caches) == B
+        assert all(int(c.n) == 0 for c in caches), \
+            "caches must be empty (chunked prefill: prefill_chunk_state)"
+        lens = [T] * B if lens is None else [int(x) for x in lens]
+        table = _append_rows(k, v, caches, lens)
+        if not (table is not None and window is None and
+                all(c.kp is caches[0].kp for c in caches)):
+            table = None
+    if table is not None:
+        # keys back from the pages just written: no packed copy of K/V
+        c0 = caches[0]
+        attn.prefill_varlen(qp, None, None, cu, 1.0 / D, window=w,
+                            max_seqlen=T, k_pool=c0.kp, v_pool=c0.vp,
+                            block_table=table.contiguous(), rel=relp,
+                            out=out.view(B * T, H, D), return_lse=False,
+                            reject=reject)
+        return out
+    kp = _packed(k, B, T, HK, D)
+    vp = _packed(v, B, T, HK, D)
+    attn.prefill_varlen(qp, kp, vp, cu, 1.0 / D, window=w, max_seqlen=T,
+                        rel=relp, out=out.view(B * T, H, D),
                         return_lse=False, reject=reject)
     return out
 
@@ -232,11 +306,14 @@ def prefill_chunk_state(q, k, v, rel, cache):
     n = int(cache.n)
     prior = torch.tensor([n], dtype=torch.int32, device=dev)
     cu = torch.tensor([0, T], dtype=torch.int32, device=dev)
-    if hasattr(cache, "table_dev_row"):
+    if hasattr(cache, "kp"):
         ps = cache.page_size
-        assert ps == PAGE and cache.table_dev_row is not None
+        assert ps == PAGE
         cache.ensure_pages((n + T - 1) // ps)
-        table = cache.table_dev_row.to(torch.int32)[None].contiguous()
+        if getattr(cache, "table_dev_row", None) is not None:
+            table = cache.table_dev_row.to(torch.int32)[None].contiguous()
+        else:                                    # a PagedKV with its own pool
+            table = torch.tensor([cache.table], dtype=torch.int32, device=dev)
         kp, vp, wrap, window = cache.kp, cache.vp, 0, 0
     else:
         W = cache.k.shape[0]

@@ -104,6 +104,144 @@ __global__ __launch_bounds__(256) void kv_write_paged_kernel(
   }
 }
 
+// ---- channel-major input ------------------------------------------------
+// K / V whose tokens are contiguous and whose head_dim is strided (the
+// sconv's output layout in the reference's prefill, where the cache append
+// receives views [T, HK, D] with strides (1, D*T, T): model.py:486-512,
+// experiments/DEADENDS.md:631-645). A work-group moves 64 tokens x 128
+// dims of one KV head for K and for V: coalesced 16-byte loads along the
+// tokens of one dim into an LDS tile [128 dims][64 tokens], then transposed
+// LDS reads (ds_read_b64_tr_b16: 4 dims of one token per lane and read)
+// give each lane 8 dims of one token, stored as one 16-byte chunk of the
+// token's page row. Bit-exact.
+//
+// LDS rows are 128 bytes (64 tokens of one dim), two per 256-byte bank row;
+// the 16-byte chunk c of dim row d sits at slot c ^ swz(d), swz(d) =
+// h((d >> 1) & 7), h(x) = ((x & 1) << 2) | (x >> 1): the 8 rows of one
+// parity among 16 consecutive rows get distinct slots (row-chunk writes do
+// not conflict), and rows d0, d0 + 2 (d0 % 4 == 0) get slots from opposite
+// halves (a transposed read of 4 rows x 32 tokens does not conflict).
+constexpr int kCmTok = 64;     // tokens per work-group
+constexpr int kCmD = 128;      // head_dim of the channel-major path
+
+__device__ __forceinline__ uint32_t cm_slot(int d, int c) {
+  const int x = (d >> 1) & 7;
+  return (uint32_t)(c ^ (((x & 1) << 2) | (x >> 1)));
+}
+
+// grid (tiles, num_seqs, HKV), 256 threads
+__global__ __launch_bounds__(256) void kv_write_paged_cm_kernel(
+    const __bf16* __restrict__ k, const __bf16* __restrict__ v, int64_t k_sh,
+    int64_t k_sd, int64_t v_sh, int64_t v_sd,
+    const int32_t* __restrict__ cu_seqlens,
+    const int32_t* __restrict__ start_pos,
+    const int32_t* __restrict__ block_table, int64_t bt_stride,
+    int table_wrap, int page_size, int HKV, u32x4* __restrict__ kp,
+    u32x4* __restrict__ vp, int64_t num_pages) {
+  __shared__ __align__(16) char tile[2][kCmD * kCmTok * 2];   // K, V: 32 KB
+  const int seq = blockIdx.y;
+  const int h = blockIdx.z;
+  int t0 = seq, len = 1;
+  if (cu_seqlens != nullptr) {
+    t0 = cu_seqlens[seq];
+    len = cu_seqlens[seq + 1] - t0;
+  }
+  // tiles start at a multiple of 8 tokens (16-byte aligned loads): the first
+  // one may hold up to 7 rows before the run, the last rows after it; those
+  // are loaded (inside the tensor, or zeros past the run's last row) and
+  // never stored
+  const int a0 = (t0 & ~7) + kCmTok * (int)blockIdx.x;
+  if (a0 >= t0 + len) return;
+  const int tid = threadIdx.x;
+  // one resource per head: rows up to the run's end; the last dim's rows
+  // after it read as zeros. The range check is per dword (a dword that
+  // straddles the end reads as zero), so the range is rounded up to the
+  // dword holding the run's last token: at most 2 bytes past the run,
+  // never past a mapped page (page ends are dword aligned)
+  const uint32_t nrec_k =
+      (uint32_t)((((int64_t)(kCmD - 1) * k_sd + t0 + len) * 2 + 3) & ~3ll);
+  const uint32_t nrec_v =
+      (uint32_t)((((int64_t)(kCmD - 1) * v_sd + t0 + len) * 2 + 3) & ~3ll);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<__bf16*>(k + (int64_t)h * k_sh), (short)0, nrec_k,
+      0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<__bf16*>(v + (int64_t)h * v_sh), (short)0, nrec_v,
+      0x00020000);
+  // loads: chunk c = tid + 256 j -> dim c >> 3, tokens a0 + 8 (c & 7) .. +7
+  u32x4 xk[4], xv[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = tid + 256 * j;
+    const int d = c >> 3, t8 = c & 7;
+    xk[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+        rk, (int)((d * k_sd + a0 + 8 * t8) * 2), 0, 0));
+    xv[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+        rv, (int)((d * v_sd + a0 + 8 * t8) * 2), 0, 0));
+  }
+  const uint32_t lk =
+      (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)tile[0]);
+  const uint32_t lv =
+      (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)tile[1]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = tid + 256 * j;
+    const int d = c >> 3, t8 = c & 7;
+    const uint32_t off = d * 128 + 16 * cm_slot(d, t8);
+    lds_st128(lk + off, xk[j]);
+    lds_st128(lv + off, xv[j]);
+  }
+  __syncthreads();
+  // transposed reads: 16-lane group G (of 16) takes tokens 16 (G & 3) ..+15
+  // and dims 32 (G >> 2) .. +31; source lane s = 4 jj + m of the group names
+  // dim row d0 + jj, tokens 16 (G & 3) + 4 m .. +3, and lane i then holds
+  // dims d0 .. d0 + 3 of token 16 (G & 3) + i
+  const int lane = tid & 63;
+  const int G = (tid >> 6) * 4 + (lane >> 4);
+  const int i = lane & 15;
+  const int jj = i >> 2, m = i & 3;
+  const int tb = G & 3;
+  const int tok = 16 * tb + i;                    // token of this lane
+  const int chunk = 2 * tb + (m >> 1);            // 16-byte chunk it names
+  const int gtok = a0 + tok;
+  const int p0 = start_pos[seq];
+  const int keep_from = table_wrap > 0 ? p0 + len - table_wrap * page_size : 0;
+  const int pos = p0 + (gtok - t0);
+  const bool live = gtok >= t0 && gtok < t0 + len && pos >= 0 &&
+                    pos >= keep_from;
+  int page = -1;
+  if (live) {
+    int lp = pos / page_size;
+    if (table_wrap > 0) lp %= table_wrap;
+    if ((int64_t)lp < bt_stride) page = block_table[(int64_t)seq * bt_stride + lp];
+  }
+  const int64_t D16 = kCmD / 8;
+  const int64_t row = (int64_t)page * page_size + pos % page_size;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int dq = 32 * (G >> 2) + 8 * q;
+    u32x4 ok, ov;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int d = dq + 4 * half + jj;         // the row this lane names
+      const uint32_t off = d * 128 + 16 * cm_slot(d, chunk) + 8 * (m & 1);
+      const bf16x4 a = lds_tr16(lk + off);
+      const bf16x4 b = lds_tr16(lv + off);
+      const u32x2 ua = __builtin_bit_cast(u32x2, a);
+      const u32x2 ub = __builtin_bit_cast(u32x2, b);
+      ok[2 * half] = ua[0];
+      ok[2 * half + 1] = ua[1];
+      ov[2 * half] = ub[0];
+      ov[2 * half + 1] = ub[1];
+    }
+    if (page >= 0 && page < num_pages) {
+      const int64_t dst = (row * HKV + h) * D16 + (dq >> 3);
+      kp[dst] = ok;
+      vp[dst] = ov;
+    }
+  }
+}
+
 int check_kv_common(const void* k, const void* v, int64_t k_st, int64_t k_sh,
                     int64_t v_st, int64_t v_sh, int HKV, int D,
                     const void* kp, const void* vp) {
@@ -158,7 +296,8 @@ extern "C" int tmopt_kv_write_slots(const void* k, const void* v,
 
 extern "C" int tmopt_kv_write_paged(
     const void* k, const void* v, int64_t k_stride_tok, int64_t k_stride_head,
-    int64_t v_stride_tok, int64_t v_stride_head, const int32_t* cu_seqlens,
+    int64_t k_stride_dim, int64_t v_stride_tok, int64_t v_stride_head,
+    int64_t v_stride_dim, const int32_t* cu_seqlens,
     const int32_t* start_pos, int num_seqs, int max_seqlen,
     const int32_t* block_table, int64_t bt_stride, int table_wrap,
     int page_size, int HKV, int D, void* k_pool, void* v_pool,
@@ -180,6 +319,43 @@ extern "C" int tmopt_kv_write_paged(
   TMOPT_REQUIRE(max_seqlen >= 0, TMOPT_EINVAL, "kv_write_paged: max_seqlen=%d",
                 max_seqlen);
   if (max_seqlen == 0) return TMOPT_OK;
+  if (k_stride_dim != 1 || v_stride_dim != 1) {
+    // channel-major rows: tokens contiguous, head_dim strided
+    TMOPT_REQUIRE(k && v && k_pool && v_pool, TMOPT_EINVAL,
+                  "kv_write_paged: null tensor pointer");
+    TMOPT_REQUIRE(D == kCmD && HKV > 0 && HKV <= 65535, TMOPT_EUNSUPPORTED,
+                  "kv_write_paged: channel-major rows need D=%d (got %d)",
+                  kCmD, D);
+    TMOPT_REQUIRE(k_stride_tok == 1 && v_stride_tok == 1 &&
+                      k_stride_dim % 8 == 0 && v_stride_dim % 8 == 0 &&
+                      k_stride_head % 8 == 0 && v_stride_head % 8 == 0 &&
+                      ((uintptr_t)k | (uintptr_t)v) % 16 == 0,
+                  TMOPT_EUNSUPPORTED,
+                  "kv_write_paged: strided head_dim needs contiguous tokens "
+                  "and 16-byte aligned dim rows (strides tok=%lld dim=%lld "
+                  "head=%lld)", (long long)k_stride_tok,
+                  (long long)k_stride_dim, (long long)k_stride_head);
+    TMOPT_REQUIRE(((uintptr_t)k_pool | (uintptr_t)v_pool) % 16 == 0,
+                  TMOPT_EINVAL, "kv_write_paged: pools must be 16-byte aligned");
+    // a dim row holds the tokens of every run (token index < dim stride),
+    // so a head's 128 rows span 128 strides: 32-bit byte offsets
+    TMOPT_REQUIRE(((int64_t)kCmD * (k_stride_dim > v_stride_dim
+                                        ? k_stride_dim
+                                        : v_stride_dim) +
+                   2 * kCmTok) * 2 < (1ll << 31),
+                  TMOPT_EUNSUPPORTED,
+                  "kv_write_paged: a head's channel-major span must stay "
+                  "below 2 GiB");
+    const int64_t tiles = ((int64_t)max_seqlen + 7 + kCmTok - 1) / kCmTok;
+    hipLaunchKernelGGL(kv_write_paged_cm_kernel,
+                       dim3((unsigned)tiles, num_seqs, HKV), dim3(256), 0,
+                       (hipStream_t)stream, (const __bf16*)k,
+                       (const __bf16*)v, k_stride_head, k_stride_dim,
+                       v_stride_head, v_stride_dim, cu_seqlens, start_pos,
+                       block_table, bt_stride, table_wrap, page_size, HKV,
+                       (u32x4*)k_pool, (u32x4*)v_pool, num_pages);
+    return check_launch("kv_write_paged (channel-major)");
+  }
   int st = check_kv_common(k, v, k_stride_tok, k_stride_head, v_stride_tok,
                            v_stride_head, HKV, D, k_pool, v_pool);
   if (st) return st;

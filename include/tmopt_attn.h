@@ -190,6 +190,28 @@ int tmopt_attn_decode_paged(const void* q, const void* k_pool,
                             size_t workspace_bytes, tmopt_stream_t stream);
 
 /*
+ * Paged decode over a sliding-window layer's ring pool as the reference
+ * engine hands it to attn_swa (engine/pyengine/kernels/attn_swa.py:
+ * 120-141): the SwaPool rows (engine/pyengine/kv.py:215-235) k_pool /
+ * v_pool [S+1, W, HKV, D] viewed as (S+1) * ring_pages pages of 16 tokens
+ * (W = 16 * ring_pages), slots [B] int64 ring rows, pos [B] int64 query
+ * positions. Row b attends keys max(0, pos[b] - window + 1) .. pos[b],
+ * which sit at ring slot p % W of row slots[b] (RingKV, kv.py:75-76);
+ * 0 < window <= W. No block table or lengths need building per call: the
+ * kernels read slots and pos in place. Otherwise as
+ * tmopt_attn_decode_paged (num_pages = (S+1) * ring_pages), with the same
+ * results.
+ */
+int tmopt_attn_decode_ring(const void* q, const void* k_pool,
+                           const void* v_pool, const int64_t* slots,
+                           int ring_pages, const int64_t* pos, int B, int HQ,
+                           int HKV, int D, int64_t num_pages, int window,
+                           float scale, const void* rel, int rel_extent,
+                           int min_pages, int num_workgroups, void* out,
+                           float* lse, void* workspace,
+                           size_t workspace_bytes, tmopt_stream_t stream);
+
+/*
  * tmopt_attn_decode_paged without the workspace argument: the same kernels
  * and results, with the scratch taken from a static device array inside the
  * library (16 MiB per GPU, held until the process ends). This entry point

@@ -178,3 +178,27 @@ def test_attn_prefill_fused_populates_caches(tm, dev, kind):
                                 table_wrap=E // 16, lo=max(0, n - E))
             rows = rows[max(0, n - E):]
         assert np.array_equal(got, kv_ref.as_u16(rows)), f"cache row {i}"
+
+
+def test_attn_swa_model_shape_ring_grid(tm, dev):
+    """attn_swa at the model's SWA shape (B = 64, W = E = 512, 64Q/16KV):
+    full rings and short ones (positions 0..30000), so the ring-aligned
+    work split (whole rings per work-group) meets rows of every length;
+    every row against the oracle's model semantics."""
+    g = torch.Generator().manual_seed(18)
+    B, W, HK, D, HQ = 64, 512, 16, 128, 64
+    pos = torch.randint(0, 30000, (B,), generator=g)
+    pos[:8] = torch.tensor([0, 1, 15, 16, 255, 510, 511, 512])
+    slots = torch.randperm(B, generator=g)
+    pool_k = (torch.randn((B + 1, W, HK, D), generator=g) * 0.5).to(
+        torch.bfloat16)
+    pool_v = (torch.randn((B + 1, W, HK, D), generator=g) * 0.5).to(
+        torch.bfloat16)
+    q = torch.randn((B, HQ, D), generator=g).to(torch.bfloat16)
+    rel = (torch.randn((B, HQ, W), generator=g) * 0.5).to(torch.bfloat16)
+    ref, _ = attn_ref.decode_reference_semantics(q, pool_k, pool_v, slots,
+                                                 pos, rel, W)
+    out = tm.attn_swa(q.to(dev), pool_k.to(dev), pool_v.to(dev),
+                      slots.to(dev), pos.to(dev), rel.to(dev))
+    torch.cuda.synchronize()
+    assert_out_close(out, ref, "attn_swa model shape")

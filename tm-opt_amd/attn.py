@@ -195,6 +195,45 @@ def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
     return out, lse
 
 
+def decode_ring(q, pool_k, pool_v, slots, pos, scale, window, rel=None,
+                min_pages=8, num_workgroups=0, out=None, lse=None,
+                workspace=None, return_lse=False):
+    """Paged decode over a ring pool as the engine holds it: pool_k/pool_v
+    [S, W, HKV, D] bf16 (SwaPool rows), slots [B] int64 ring rows, pos [B]
+    int64 query positions, 0 < window <= W; the kernels read slots and pos
+    in place (no block table or lengths built per call).
+    Returns (out [B, HQ, D] bf16, lse [B, HQ] fp32 or None).
+    Reference: engine/pyengine/kernels/attn_swa.py:120-141, kv.py:215-235."""
+    B, HQ, D = q.shape
+    assert q.dtype == torch.bfloat16 and q.is_contiguous()
+    assert pool_k.is_contiguous() and pool_v.is_contiguous()
+    assert pool_k.shape == pool_v.shape and pool_k.dim() == 4
+    S, W, HKV, Dk = pool_k.shape
+    assert W % PAGE_SIZE == 0 and Dk == D and HQ % HKV == 0
+    assert 0 < window <= W
+    assert slots.dtype == torch.int64 and slots.shape == (B,)
+    assert pos.dtype == torch.int64 and pos.shape == (B,)
+    assert slots.is_contiguous() and pos.is_contiguous()
+    if rel is not None:
+        assert rel.dtype == torch.bfloat16 and rel.is_contiguous()
+        assert rel.shape[:2] == (B, HQ)
+    per = W // PAGE_SIZE
+    dev = q.device
+    if out is None:
+        out = torch.empty_like(q)
+    if lse is None and return_lse:
+        lse = torch.empty((B, HQ), dtype=torch.float32, device=dev)
+    if workspace is None:
+        workspace = decode_workspace(B, HQ, HKV, dev, num_workgroups)
+    _lib.call("tmopt_attn_decode_ring", _ptr(q), _ptr(pool_k), _ptr(pool_v),
+              _ptr(slots), per, _ptr(pos), B, HQ, HKV, D, S * per,
+              int(window), float(scale), _ptr(rel),
+              0 if rel is None else rel.shape[2], int(min_pages),
+              int(num_workgroups), _ptr(out), _ptr(lse), _ptr(workspace),
+              workspace.numel() * workspace.element_size(), _stream(dev))
+    return out, lse
+
+
 def decode_paged_noalloc(q, k_pool, v_pool, block_table, ctx_lens, scale,
                          out, lse=None, window=0, table_wrap=0, rel=None,
                          min_pages=8, num_workgroups=0):

@@ -81,6 +81,13 @@ struct DecodeArgs {
   int bt_width;      // entries a row may be read at: min(bt_stride, 2^31-1)
   int table_wrap;
   const int32_t* ctx_lens;
+  // the engine's own index tensors instead of a block table and lengths
+  // (tmopt_attn_decode_ring): kind 2 = ring slots [B] int64 (page
+  // slot * table_wrap + lp % table_wrap) and pos64 [B] int64 query
+  // positions (keys = pos + 1)
+  int bt_kind;
+  const int64_t* rows64;
+  const int64_t* pos64;
   int B, HQ, HKV;
   int num_pages;     // clamped to INT32_MAX: page ids are int32
   int window;
@@ -105,12 +112,25 @@ __device__ __forceinline__ int vis_pages(int n, int window) {
   return (n + kPS - 1) / kPS - vis_lo(n, window) / kPS;
 }
 
+// keys of sequence b (its query sits at position n - 1)
+template <int KIND>
+__device__ __forceinline__ int seq_n(const DecodeArgs& a, int b) {
+  if constexpr (KIND != 0) return (int)(as_const(a.pos64)[b] + 1);
+  return as_const(a.ctx_lens)[b];
+}
+
+template <int KIND>
 __device__ __forceinline__ int page_id(const DecodeArgs& a, int b, int lp) {
   const int idx = a.table_wrap > 0 ? lp % a.table_wrap : lp;
-  // a logical page past the row's width has no entry: its keys are absent
-  // (reading on would return the next row's page ids)
-  if ((unsigned)idx >= (unsigned)a.bt_width) return -1;
-  const int v = as_const(a.bt)[(int64_t)b * a.bt_stride + idx];
+  int v;
+  if constexpr (KIND == 2) {
+    v = (int)as_const(a.rows64)[b] * a.table_wrap + idx;
+  } else {
+    // a logical page past the row's width has no entry: its keys are absent
+    // (reading on would return the next row's page ids)
+    if ((unsigned)idx >= (unsigned)a.bt_width) return -1;
+    v = as_const(a.bt)[(int64_t)b * a.bt_stride + idx];
+  }
   // one unsigned 32-bit compare: stays on the scalar unit (a 64-bit signed
   // compare would borrow VGPRs that in-flight loads may still own)
   return (unsigned)v < (unsigned)a.num_pages ? v : -1;
@@ -215,7 +235,7 @@ __device__ __forceinline__ void issue_step(StepBuf<REL>& buf,
 // DEPTH: steps whose loads are in flight or being consumed; DEPTH - 1 steps
 // (16 KB each per wave) stream in while one is computed. One work-group per
 // CU (one wave per SIMD, the whole register file per wave).
-template <int REP, bool REL, int DEPTH>
+template <int REP, bool REL, int DEPTH, int KIND>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
 void decode_kernel(DecodeArgs a) {
   extern __shared__ __align__(16) char smem[];
@@ -237,7 +257,7 @@ void decode_kernel(DecodeArgs a) {
     int carry = 0;
     for (int b0 = 0; b0 < a.B; b0 += blockDim.x) {
       const int b = b0 + threadIdx.x;
-      const int v = b < a.B ? vis_pages(as_const(a.ctx_lens)[b], a.window) : 0;
+      const int v = b < a.B ? vis_pages(seq_n<KIND>(a, b), a.window) : 0;
       // inclusive scan over the wave by DPP (VALU, no LDS round trips):
       // within each 16-lane row by shifts of 1, 2, 4, 8, then row 0's
       // total into row 1 and row 2's into row 3, then rows 0-1's total into
@@ -302,7 +322,7 @@ void decode_kernel(DecodeArgs a) {
     cb = __builtin_amdgcn_readfirstlane(lo);
   }
   int seq_start = __builtin_amdgcn_readfirstlane(pref[cb]);
-  int cur_n = as_const(a.ctx_lens)[cb];
+  int cur_n = seq_n<KIND>(a, cb);
   int seq_end = seq_start + vis_pages(cur_n, a.window);
   int cu = u0;
   int last_b = -1;  // sequence of the previous step handed out
@@ -315,7 +335,7 @@ void decode_kernel(DecodeArgs a) {
     while (seq_end <= cu) {
       ++cb;
       seq_start = seq_end;
-      cur_n = as_const(a.ctx_lens)[cb];
+      cur_n = seq_n<KIND>(a, cb);
       seq_end = seq_start + vis_pages(cur_n, a.window);
     }
     const int piece_end = min(seq_end, u1);
@@ -325,8 +345,8 @@ void decode_kernel(DecodeArgs a) {
     st.s0 = seq_start;
     st.s1 = seq_end;
     st.pg = vis_lo(cur_n, a.window) / kPS + (cu - seq_start);
-    st.phys0 = page_id(a, cb, st.pg);
-    st.phys1 = cnt > 1 ? page_id(a, cb, st.pg + 1) : -1;
+    st.phys0 = page_id<KIND>(a, cb, st.pg);
+    st.phys1 = cnt > 1 ? page_id<KIND>(a, cb, st.pg + 1) : -1;
     cu += cnt;
     st.last = cu == piece_end;
     st.first = cb != last_b;
@@ -626,15 +646,22 @@ size_t ws_layout(int B, int HQ, int G, size_t* off_lse, size_t* off_geo) {
   return o_bytes + l_bytes + g_bytes;
 }
 
+template <int REP, int KIND>
+void launch_kind(const DecodeArgs& a, dim3 grid, int nw, size_t lds,
+                 hipStream_t st) {
+  if (a.rel)
+    hipLaunchKernelGGL((decode_kernel<REP, true, kDeep, KIND>), grid,
+                       dim3(64 * nw), lds, st, a);
+  else
+    hipLaunchKernelGGL((decode_kernel<REP, false, kDeep, KIND>), grid,
+                       dim3(64 * nw), lds, st, a);
+}
+
 template <int REP>
 void launch(const DecodeArgs& a, int G, int nw, size_t lds, hipStream_t st) {
-  dim3 grid(G, a.HKV / nw);
-  if (a.rel)
-    hipLaunchKernelGGL((decode_kernel<REP, true, kDeep>), grid, dim3(64 * nw),
-                       lds, st, a);
-  else
-    hipLaunchKernelGGL((decode_kernel<REP, false, kDeep>), grid,
-                       dim3(64 * nw), lds, st, a);
+  const dim3 grid(G, a.HKV / nw);
+  if (a.bt_kind == 2) launch_kind<REP, 2>(a, grid, nw, lds, st);
+  else launch_kind<REP, 0>(a, grid, nw, lds, st);
 }
 
 // ---- static scratch of the allocation-free entry point -------------------
@@ -689,19 +716,25 @@ extern "C" size_t tmopt_attn_decode_workspace_size(int B, int HQ, int HKV,
   return ws_layout(B, HQ, G, nullptr, nullptr);
 }
 
-extern "C" int tmopt_attn_decode_paged(
-    const void* q, const void* k_pool, const void* v_pool,
-    const int32_t* block_table, int64_t bt_stride, int table_wrap,
-    const int32_t* ctx_lens, int B, int HQ, int HKV, int D, int page_size,
-    int64_t num_pages, int window, float scale, const void* rel,
-    int rel_extent, int min_pages, int num_workgroups, void* out, float* lse,
-    void* workspace, size_t workspace_bytes, tmopt_stream_t stream) {
-  clear_error();
+// The decode launch behind both entry points: `kind` 0 = int32 block table
+// + int32 lengths (block_table, ctx_lens), 2 = ring slots + int64 positions
+// (rows64, pos64). (Per-token flat rows read in place, one page id per
+// 128 bytes, measured 17% slower than an int32 table at B = 64: every
+// page lookup missed the scalar cache ahead of the step's loads.)
+static int decode_impl(
+    int kind, const void* q, const void* k_pool, const void* v_pool,
+    const int32_t* block_table, const int64_t* rows64, int64_t bt_stride,
+    int table_wrap, const int32_t* ctx_lens, const int64_t* pos64, int B,
+    int HQ, int HKV, int D, int page_size, int64_t num_pages, int window,
+    float scale, const void* rel, int rel_extent, int min_pages,
+    int num_workgroups, void* out, float* lse, void* workspace,
+    size_t workspace_bytes, tmopt_stream_t stream) {
   if (B == 0) return TMOPT_OK;
   TMOPT_REQUIRE(B > 0, TMOPT_EINVAL, "decode: B=%d", B);
   TMOPT_REQUIRE(B <= kMaxB, TMOPT_EUNSUPPORTED, "decode: B=%d above %d", B,
                 kMaxB);
-  TMOPT_REQUIRE(q && k_pool && v_pool && block_table && ctx_lens && out,
+  TMOPT_REQUIRE(q && k_pool && v_pool && out &&
+                    (kind == 0 ? block_table && ctx_lens : rows64 && pos64),
                 TMOPT_EINVAL, "decode: null tensor pointer");
   TMOPT_REQUIRE(D == kD, TMOPT_EUNSUPPORTED, "decode: D=%d (only 128)", D);
   TMOPT_REQUIRE(page_size == kPS, TMOPT_EUNSUPPORTED,
@@ -753,6 +786,9 @@ extern "C" int tmopt_attn_decode_paged(
   a.bt_width = bt_stride > 0x7fffffff ? 0x7fffffff : (int)bt_stride;
   a.table_wrap = table_wrap;
   a.ctx_lens = ctx_lens;
+  a.bt_kind = kind;
+  a.rows64 = rows64;
+  a.pos64 = pos64;
   a.B = B;
   a.HQ = HQ;
   a.HKV = HKV;
@@ -785,6 +821,38 @@ extern "C" int tmopt_attn_decode_paged(
   hipLaunchKernelGGL(decode_combine_kernel, dim3(B, (HQ + 7) / 8), dim3(256),
                      0, st, a);
   return check_launch("decode_combine");
+}
+
+extern "C" int tmopt_attn_decode_paged(
+    const void* q, const void* k_pool, const void* v_pool,
+    const int32_t* block_table, int64_t bt_stride, int table_wrap,
+    const int32_t* ctx_lens, int B, int HQ, int HKV, int D, int page_size,
+    int64_t num_pages, int window, float scale, const void* rel,
+    int rel_extent, int min_pages, int num_workgroups, void* out, float* lse,
+    void* workspace, size_t workspace_bytes, tmopt_stream_t stream) {
+  clear_error();
+  return decode_impl(0, q, k_pool, v_pool, block_table, nullptr, bt_stride,
+                     table_wrap, ctx_lens, nullptr, B, HQ, HKV, D, page_size,
+                     num_pages, window, scale, rel, rel_extent, min_pages,
+                     num_workgroups, out, lse, workspace, workspace_bytes,
+                     stream);
+}
+
+extern "C" int tmopt_attn_decode_ring(
+    const void* q, const void* k_pool, const void* v_pool,
+    const int64_t* slots, int ring_pages, const int64_t* pos, int B, int HQ,
+    int HKV, int D, int64_t num_pages, int window, float scale,
+    const void* rel, int rel_extent, int min_pages, int num_workgroups,
+    void* out, float* lse, void* workspace, size_t workspace_bytes,
+    tmopt_stream_t stream) {
+  clear_error();
+  TMOPT_REQUIRE(ring_pages > 0, TMOPT_EINVAL, "decode_ring: ring_pages=%d",
+                ring_pages);
+  return decode_impl(2, q, k_pool, v_pool, nullptr, slots, ring_pages,
+                     ring_pages, nullptr, pos, B, HQ, HKV, D, kPS, num_pages,
+                     window, scale, rel, rel_extent, min_pages,
+                     num_workgroups, out, lse, workspace, workspace_bytes,
+                     stream);
 }
 
 extern "C" int tmopt_attn_decode_paged_noalloc(

@@ -85,6 +85,34 @@ __device__ __forceinline__ void dma_b128(i32x4 rsrc, uint32_t lds, int voff) {
       : "memory", "m0");
 }
 
+// The same DMA through the compiler's LDS-DMA builtin, so that the
+// compiler counts it among the wave's outstanding loads. Kernels that also
+// issue ordinary loads inside the tile loop (the fused bias) need that:
+// without it the compiler, blind to the DMA, waits with vmcnt(0) for its
+// own loads and so drains the tiles prefetched behind them.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+template <bool VIS>
+__device__ __forceinline__ auto mk_rsrc(const void* base, uint32_t bytes) {
+  if constexpr (VIS)
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base),
+                                             (short)0, (int)bytes,
+                                             0x00020000);
+  else
+    return make_rsrc(base, bytes);
+}
+
+// (overloads on the resource type: the builtin's resource type cannot be
+// a deduced template parameter)
+__device__ __forceinline__ void dma(rsrc_t rsrc, uint32_t lds, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rsrc, (__attribute__((address_space(3))) void*)(uintptr_t)lds, 16,
+      (unsigned)voff, 0, 0, 0);
+}
+__device__ __forceinline__ void dma(i32x4 rsrc, uint32_t lds, int voff) {
+  dma_b128(rsrc, lds, voff);
+}
+
 // wait until at most N vector-memory loads of this wave are in flight
 template <int N>
 __device__ __forceinline__ void wait_vm() {
@@ -279,15 +307,16 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   const uint32_t lds0 =
       (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)smem);
   // packed rows of the run (keys 0.. of the run itself)
-  i32x4 rk = {0, 0, 0, 0}, rv = {0, 0, 0, 0};
+  constexpr bool VIS = REL;   // DMA the compiler can see (see dma())
+  auto rk = mk_rsrc<VIS>(nullptr, 0u), rv = mk_rsrc<VIS>(nullptr, 0u);
   int kst_b = 0, vst_b = 0, klane_p = 0, vlane_p = 0;
   if constexpr (OWN) {
     kst_b = (int)(a.k_st * 2);
     vst_b = (int)(a.v_st * 2);
-    rk = make_rsrc(a.k + (int64_t)t0 * a.k_st + (int64_t)kvh * a.k_sh,
-                   (uint32_t)(((int64_t)(len - 1) * a.k_st + kD) * 2));
-    rv = make_rsrc(a.v + (int64_t)t0 * a.v_st + (int64_t)kvh * a.v_sh,
-                   (uint32_t)(((int64_t)(len - 1) * a.v_st + kD) * 2));
+    rk = mk_rsrc<VIS>(a.k + (int64_t)t0 * a.k_st + (int64_t)kvh * a.k_sh,
+                      (uint32_t)(((int64_t)(len - 1) * a.k_st + kD) * 2));
+    rv = mk_rsrc<VIS>(a.v + (int64_t)t0 * a.v_st + (int64_t)kvh * a.v_sh,
+                      (uint32_t)(((int64_t)(len - 1) * a.v_st + kD) * 2));
     klane_p = grp * kst_b + 16 * kchunk;
     vlane_p = grp * vst_b + 16 * vchunk;
   }
@@ -323,9 +352,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
       const uint32_t nrec = valid ? (uint32_t)((r_hi - r_lo) * row_b) : 0u;
       const int64_t pofs = valid ? (int64_t)pg * page_b + r_lo * row_b : 0;
       const int roff = ((key0 & (kPage - 1)) - r_lo) * row_b;
-      dma_b128(make_rsrc(reinterpret_cast<const char*>(a.kpool) + pofs, nrec),
+      dma(mk_rsrc<VIS>(reinterpret_cast<const char*>(a.kpool) + pofs,
+                            nrec),
                dk, klane + roff);
-      dma_b128(make_rsrc(reinterpret_cast<const char*>(a.vpool) + pofs, nrec),
+      dma(mk_rsrc<VIS>(reinterpret_cast<const char*>(a.vpool) + pofs,
+                            nrec),
                dv, vlane + roff);
     }
   };
@@ -333,8 +364,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // run end are outside the resource: zeros)
   auto own_dma = [&](int j, uint32_t dk, uint32_t dv) {
     if constexpr (OWN) {
-      dma_b128(rk, dk, klane_p + j * kst_b);
-      dma_b128(rv, dv, vlane_p + j * vst_b);
+      dma(rk, dk, klane_p + j * kst_b);
+      dma(rv, dv, vlane_p + j * vst_b);
     }
   };
 
@@ -430,68 +461,86 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   [[maybe_unused]] const int rrow_b =
       REL ? rel_mis + l32 * (int)(a.r_st * 2) : 0;
 
+  // The fused bias of a key tile, loaded one softmax ahead (bias_issue)
+  // and applied in the softmax (bias_apply). The lane's keys come in runs
+  // of four (key0 .. key0+3, dist d0 .. d0-3), whose four bf16 values are
+  // adjacent in the row: the three dwords from the one holding rel[d0-3],
+  // realigned by 0 or 2 bytes. The range check is per dword and the
+  // resource ends at a dword boundary, so every value of the rows arrives;
+  // the whole offset goes in the lane register, where the check sees it.
+  // Every call issues exactly 8 loads (a tile outside the band or past the
+  // run reads nothing), so the wave's load counts stay fixed: the waits
+  // for them never reach the tile DMA issued after them.
+  typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+  [[maybe_unused]] u32x3 rb[8];
+  [[maybe_unused]] auto bias_issue = [&](int kt) {
+    if constexpr (REL) {
+      const bool band_tile = kt < k_hi && pos_lo - (kt + kBN - 1) < a.rel_extent;
+      // byte offset of rel[d0 - 3] for kb = g = 0, opaque to the compiler
+      // so that the eight offsets are derived from it here rather than
+      // hoisted out of the key loop as eight live registers
+      int base = rrow_b + 2 * (qpos - kt - 4 * h2 - 3);
+      asm volatile("" : "+v"(base));
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int b4 = (base - 64 * kb - 16 * g) & ~3;
+          // before the first row (row 0 near dist 0): from the row start,
+          // shifted back into place by bias_apply
+          int off = band_tile ? (b4 < 0 ? 0 : b4) : 0x7ffffff0;
+          asm volatile("" : "+v"(off));
+          rb[4 * kb + g] = __builtin_bit_cast(
+              u32x3, __builtin_amdgcn_raw_buffer_load_b96(rrel, off, 0, 0));
+        }
+    }
+  };
+  // the scores move to the log2 domain: s*scale*log2e + rel*log2e,
+  // rel[q, h, dist] for 0 <= dist < E, zero outside
+  [[maybe_unused]] auto bias_apply = [&](f32x16 (&s)[2], int kt) {
+    if constexpr (REL) {
+      // dist of the lane's first key for kb = g = 0 (opaque, as above)
+      int dq = qpos - kt - 4 * h2;
+      asm volatile("" : "+v"(dq));
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = dq - 32 * kb - 8 * g;
+          const int b = rrow_b + 2 * (d0 - 3);
+          const int b4 = b & ~3;
+          // dwords the load started after the one holding rel[d0-3] (only
+          // when that one lies before the row; 3 or more: every dist of
+          // the run is negative, i.e. masked)
+          const int kd = b4 < 0 ? (-b4) >> 2 : 0;
+          const uint32_t x0 = rb[4 * kb + g][0], x1 = rb[4 * kb + g][1],
+                         x2 = rb[4 * kb + g][2];
+          const uint32_t y0 = kd == 0 ? x0 : 0u;
+          const uint32_t y1 = kd == 0 ? x1 : (kd == 1 ? x0 : 0u);
+          const uint32_t y2 = kd == 0 ? x2 : (kd == 1 ? x1 : x0);
+          const uint32_t sh = (uint32_t)(b & 3);
+          const uint32_t w0 = __builtin_amdgcn_alignbyte(y1, y0, sh);
+          const uint32_t w1 = __builtin_amdgcn_alignbyte(y2, y1, sh);
+          // element 4g + i is key0 + i, dist d0 - i
+          const uint32_t hv[4] = {w1 & 0xffff0000u, w1 << 16,
+                                  w0 & 0xffff0000u, w0 << 16};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int dist = d0 - i;
+            const bool band = qok && dist >= 0 && dist < a.rel_extent;
+            const float bias = band ? __builtin_bit_cast(float, hv[i]) : 0.0f;
+            s[kb][4 * g + i] =
+                __builtin_fmaf(s[kb][4 * g + i], a.scale_log2, bias * kLog2e);
+          }
+        }
+    }
+  };
+
   // per-element mask (causal, window, run end) and, on tiles within the
   // bias band, the fused bias
   auto mask_bias = [&](f32x16 (&s)[2], int kt, bool with_bias) {
     if constexpr (REL) {
-      if (with_bias) {
-        // the scores move to the log2 domain: s*scale*log2e + rel*log2e,
-        // rel[q, h, dist] for 0 <= dist < E, zero outside. The lane's keys
-        // come in runs of four (key0 .. key0+3, dist d0 .. d0-3), whose
-        // four bf16 values are adjacent in the row: the three dwords from
-        // the one holding rel[d0-3], realigned by 0 or 2 bytes.
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int key0 = kt + 32 * kb + 8 * g + 4 * h2;
-            const int d0 = qpos - key0;
-            const int b = rrow_b + 2 * (d0 - 3);
-            // One 16-byte load from the dword holding rel[d0-3]: the range
-            // check is per dword (a dword past the range reads 0, the ones
-            // before it are returned), and the resource ends at a dword
-            // boundary, so every value of the rows arrives. The whole
-            // offset goes in the lane register, where the check sees it.
-            // Offsets before the first row occur only on the wave's first
-            // row near dist 0; then the wave takes three dword loads, one
-            // with an offset past the range for each dword before the row.
-            const int b4 = b & ~3;
-            uint32_t x0, x1, x2;
-            if (!__builtin_amdgcn_ballot_w64(b4 < 0)) {
-              int off = b4;
-              asm volatile("" : "+v"(off));
-              const u32x4 x = __builtin_bit_cast(
-                  u32x4, __builtin_amdgcn_raw_buffer_load_b128(rrel, off, 0,
-                                                               0));
-              x0 = x[0];
-              x1 = x[1];
-              x2 = x[2];
-            } else {
-              auto rel_dword = [&](int off) {
-                off = off < 0 ? 0x7ffffff0 : off;
-                asm volatile("" : "+v"(off));
-                return __builtin_amdgcn_raw_buffer_load_b32(rrel, off, 0, 0);
-              };
-              x0 = rel_dword(b4);
-              x1 = rel_dword(b4 + 4);
-              x2 = rel_dword(b4 + 8);
-            }
-            const uint32_t sh = (uint32_t)(b & 3);
-            const uint32_t w0 = __builtin_amdgcn_alignbyte(x1, x0, sh);
-            const uint32_t w1 = __builtin_amdgcn_alignbyte(x2, x1, sh);
-            // element 4g + i is key0 + i, dist d0 - i
-            const uint32_t hv[4] = {w1 & 0xffff0000u, w1 << 16,
-                                    w0 & 0xffff0000u, w0 << 16};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int dist = d0 - i;
-              const bool band = qok && dist >= 0 && dist < a.rel_extent;
-              const float bias = band ? __builtin_bit_cast(float, hv[i]) : 0.0f;
-              s[kb][4 * g + i] =
-                  __builtin_fmaf(s[kb][4 * g + i], a.scale_log2, bias * kLog2e);
-            }
-          }
-      }
+      if (with_bias) bias_apply(s, kt);
     }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -664,14 +713,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   {
     const int qrow0 = q0 + 32 * (w % QSUB);
     const int64_t qspan = ((int64_t)(len - qrow0 - 1) * a.q_st + kD) * 2;
-    const i32x4 rq = make_rsrc(
+    const auto rq = mk_rsrc<VIS>(
         a.q + (int64_t)(t0 + qrow0) * a.q_st + (int64_t)head * a.q_sh,
         qrow0 < len ? (uint32_t)qspan : 0u);
     const int qst_b = (int)(a.q_st * 2);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = 4 * i + grp;
-      dma_b128(rq, qlds + i * 1024, r * qst_b + 16 * (slot ^ (r & 15)));
+      dma(rq, qlds + i * 1024, r * qst_b + 16 * (slot ^ (r & 15)));
     }
   }
   issue_tile(0, 0);
@@ -688,33 +737,49 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   }
   __syncthreads();
   if (ntiles > 2) issue_tile(2, 2);
-  auto odd_end = [&](int t) {
-    if (t + 3 < ntiles) wait_vm<4>(); else wait_vm<0>();
+  // End of every odd slot: this wave's part of tile t+2 must be in LDS
+  // before the barrier that publishes it. Loads issued after that tile's
+  // may still fly: the DMA of tile t+3 and, with the fused bias, the bias
+  // loads of the tile after the next softmax (`bias` of them).
+  auto odd_end = [&](int t, int bias) {
+    const int n = (t + 3 < ntiles ? 4 : 0) + bias;
+    if (n == 12) wait_vm<12>();
+    else if (n == 8) wait_vm<8>();
+    else if (n == 4) wait_vm<4>();
+    else wait_vm<0>();
     __syncthreads();
   };
+  constexpr int NB = REL ? 8 : 0;   // bias loads per tile
   if (grp_id == 0) {
     scores(0, sc);
+    bias_issue(k_lo);
     softmax_phase(sc, k_lo, true);
+    bias_issue(k_lo + kBN);
     for (int t = 0; t < ntiles; ++t) {
       if (t + 3 < ntiles) issue_tile(t + 3, (t + 3) & 3);
       const bool has_next = t + 1 < ntiles;
       mfma_phase(t, has_next);
       __syncthreads();
-      if (has_next) softmax_phase(sc, k_lo + (t + 1) * kBN, false);
-      odd_end(t);
+      if (has_next) {
+        softmax_phase(sc, k_lo + (t + 1) * kBN, false);
+        bias_issue(k_lo + (t + 2) * kBN);
+      }
+      odd_end(t, has_next ? NB : 0);
     }
   } else {
     for (int t = 0; t < ntiles; ++t) {
       if (t + 3 < ntiles) issue_tile(t + 3, (t + 3) & 3);
       if (t == 0) {
         scores(0, sc);
+        bias_issue(k_lo);
         softmax_phase(sc, k_lo, true);
       } else {
         softmax_phase(sc, k_lo + t * kBN, false);
       }
+      bias_issue(k_lo + (t + 1) * kBN);
       __syncthreads();
       mfma_phase(t, t + 1 < ntiles);
-      odd_end(t);
+      odd_end(t, NB);
     }
   }
   }  // !rejected

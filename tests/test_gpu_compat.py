@@ -75,9 +75,12 @@ def test_attn_global_flat_rows(tm, dev):
 
 @pytest.mark.parametrize("window,E", [(None, 1024), (64, 64)])
 @pytest.mark.parametrize("hq,hk", [(32, 4), (64, 16)])
-def test_attn_prefill_fused_padded_batch(tm, dev, window, E, hq, hk):
+@pytest.mark.parametrize("T", [200, 77])
+def test_attn_prefill_fused_padded_batch(tm, dev, window, E, hq, hk, T):
+    """T = 200: the channel-major K/V are packed on chip (rows starting
+    mid-page: 200 % 16 = 8); T = 77 (not a multiple of 8): the copy path."""
     g = torch.Generator().manual_seed(15)
-    B, T, D = 3, 200, 128
+    B, D = 3, 128
     q = torch.randn((B, T, hq, D), generator=g).to(torch.bfloat16).transpose(
         1, 2)                                              # [B,H,T,D] view
     # K/V channel-major, as the eager sconv hands them over

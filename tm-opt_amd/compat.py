@@ -92,6 +92,44 @@ def _packed(x, B, T, H, D):
     return xt.as_strided((B * T, H, D), (xt.stride(1), xt.stride(2), 1))
 
 
+# per (B, T, device): the identity page tables of _pack_channel_major, built
+# once (a host-to-device copy from pageable memory synchronises the stream)
+_PACK_META = {}
+
+
+def _pack_channel_major(k, v, B, T, H, D):
+    """Channel-major [B, H, T, D] K/V views (the sconv output: tokens
+    contiguous) -> packed [B*T, H, D] rows, transposed on chip by the paged
+    write over an identity table: the packed buffer is a pool of 16-row
+    pages, row b starts at page (b*T)//16, slot (b*T)%16. None when the
+    layout is outside what that kernel reads (then the caller copies)."""
+    views = [x[b].transpose(0, 1) for x in (k, v) for b in range(B)]
+    if not (T % 8 == 0 and D == attn.HEAD_DIM and
+            all(attn._channel_major(x) and x.data_ptr() % 16 == 0
+                for x in views)):
+        return None
+    dev = k.device
+    P = (B * T + PAGE - 1) // PAGE
+    w = (T + PAGE - 1) // PAGE + 1
+    key = (B, T, dev)
+    meta = _PACK_META.get(key)
+    if meta is None:
+        m = torch.zeros((B, 3 + w), dtype=torch.int32)
+        for b in range(B):
+            m[b, 0] = (b * T) % PAGE
+            m[b, 2] = T
+            m[b, 3:] = torch.clamp(torch.arange(w) + (b * T) // PAGE,
+                                   max=P - 1)
+        meta = _PACK_META[key] = m.to(dev)
+    kp = torch.empty((P, PAGE, H, D), dtype=k.dtype, device=dev)
+    vp = torch.empty_like(kp)
+    for b in range(B):
+        attn.kv_write_paged(views[b], views[B + b], meta[b:b + 1, 3:],
+                            meta[b, 0:1], kp, vp, cu_seqlens=meta[b, 1:3],
+                            max_seqlen=T)
+    return (kp.view(P * PAGE, H, D)[:B * T], vp.view(P * PAGE, H, D)[:B * T])
+
+
 def _append_rows(k, v, caches, lens):
     """The prefill's cache population (model.py:507-512:
     st.cache.append(kn[i, :lens[i]], vv[i, :lens[i]])) done natively: each
@@ -207,8 +245,9 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
                             out=out.view(B * T, H, D), return_lse=False,
                             reject=reject)
         return out
-    kp = _packed(k, B, T, HK, D)
-    vp = _packed(v, B, T, HK, D)
+    kv = _pack_channel_major(k, v, B, T, HK, D)
+    kp, vp = kv if kv is not None else (_packed(k, B, T, HK, D),
+                                        _packed(v, B, T, HK, D))
     attn.prefill_varlen(qp, kp, vp, cu, 1.0 / D, window=w, max_seqlen=T,
                         rel=relp, out=out.view(B * T, H, D),
                         return_lse=False, reject=reject)

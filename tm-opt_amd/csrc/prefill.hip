@@ -43,6 +43,8 @@
 //    an equal share of every level and only one KV head's keys pass through
 //    its L2. A plain (head, run, block) grid maps runs to XCDs by index and
 //    left half of the XCDs idle for half the launch on mixed lengths.
+#include <type_traits>
+
 #include "common.h"
 
 namespace tmopt {
@@ -646,9 +648,18 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     pack_p(pw, pf);
     l_part = l_part * alpha + psum;
     // O^T holds the tiles before this one: rescale it to the new reference
+    // (in place, each product tied to its accumulator register: a plain
+    // multiply under the branch leaves the compiler a merge of two copies
+    // of O^T, which it resolves with 32 register-pair moves on every tile)
     if (!first && __builtin_amdgcn_ballot_w64(move)) {
 #pragma unroll
-      for (int db = 0; db < 4; ++db) o_acc[db] = o_acc[db] * alpha;
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          float x = o_acc[db][j];
+          asm volatile("v_mul_f32 %0, %1, %0" : "+v"(x) : "v"(alpha));
+          o_acc[db][j] = x;
+        }
     }
   };
 
@@ -656,7 +667,10 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // turn) interleaved with the scores of tile t+1 (two accumulators), the
   // V^T and K fragments read kRing - 1 MFMAs ahead (3: measured ~1% over 4
   // and 5 ahead on 4K-16K runs)
-  auto mfma_phase = [&](int t, bool with_s) {
+  auto mfma_phase = [&](int t, auto with_s_c) {
+    // (with_s as a type: one straight-line copy per case, no branch between
+    // the MFMAs)
+    constexpr bool with_s = decltype(with_s_c)::value;
     // the SIMD's issue port goes to this wave's MFMAs first; the softmax
     // wave fills the slots in between (measured ~2% over equal priority)
     __builtin_amdgcn_s_setprio(1);
@@ -750,35 +764,52 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     __syncthreads();
   };
   constexpr int NB = REL ? 8 : 0;   // bias loads per tile
+  // The first and last tiles are peeled off the loops, so that the loops
+  // hold one variant of the MFMA phase: O^T then keeps one set of
+  // registers across iterations (variants merged inside the loop made the
+  // compiler copy all 64 accumulator registers back and forth every tile).
+  constexpr std::true_type kWithS{};
+  constexpr std::false_type kNoS{};
   if (grp_id == 0) {
     scores(0, sc);
     bias_issue(k_lo);
     softmax_phase(sc, k_lo, true);
     bias_issue(k_lo + kBN);
-    for (int t = 0; t < ntiles; ++t) {
+    for (int t = 0; t + 1 < ntiles; ++t) {
       if (t + 3 < ntiles) issue_tile(t + 3, (t + 3) & 3);
-      const bool has_next = t + 1 < ntiles;
-      mfma_phase(t, has_next);
+      mfma_phase(t, kWithS);
       __syncthreads();
-      if (has_next) {
-        softmax_phase(sc, k_lo + (t + 1) * kBN, false);
-        bias_issue(k_lo + (t + 2) * kBN);
-      }
-      odd_end(t, has_next ? NB : 0);
+      softmax_phase(sc, k_lo + (t + 1) * kBN, false);
+      bias_issue(k_lo + (t + 2) * kBN);
+      odd_end(t, NB);
     }
+    mfma_phase(ntiles - 1, kNoS);
+    __syncthreads();
+    odd_end(ntiles - 1, 0);
   } else {
-    for (int t = 0; t < ntiles; ++t) {
+    if (3 < ntiles) issue_tile(3, 3);
+    scores(0, sc);
+    bias_issue(k_lo);
+    softmax_phase(sc, k_lo, true);
+    bias_issue(k_lo + kBN);
+    __syncthreads();
+    if (ntiles > 1) mfma_phase(0, kWithS);
+    else mfma_phase(0, kNoS);
+    odd_end(0, NB);
+    for (int t = 1; t + 1 < ntiles; ++t) {
       if (t + 3 < ntiles) issue_tile(t + 3, (t + 3) & 3);
-      if (t == 0) {
-        scores(0, sc);
-        bias_issue(k_lo);
-        softmax_phase(sc, k_lo, true);
-      } else {
-        softmax_phase(sc, k_lo + t * kBN, false);
-      }
+      softmax_phase(sc, k_lo + t * kBN, false);
       bias_issue(k_lo + (t + 1) * kBN);
       __syncthreads();
-      mfma_phase(t, t + 1 < ntiles);
+      mfma_phase(t, kWithS);
+      odd_end(t, NB);
+    }
+    if (ntiles > 1) {
+      const int t = ntiles - 1;
+      softmax_phase(sc, k_lo + t * kBN, false);
+      bias_issue(k_lo + (t + 1) * kBN);
+      __syncthreads();
+      mfma_phase(t, kNoS);
       odd_end(t, NB);
     }
   }

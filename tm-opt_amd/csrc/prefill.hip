@@ -142,6 +142,7 @@ struct PrefillArgs {
   int page_size;
   int HQ, HKV;
   int window;
+  float scale;
   float scale_log2;
   __bf16* out;
   int64_t o_st, o_sh;
@@ -499,7 +500,18 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   };
   // the scores move to the log2 domain: s*scale*log2e + rel*log2e,
   // rel[q, h, dist] for 0 <= dist < E, zero outside
-  [[maybe_unused]] auto bias_apply = [&](f32x16 (&s)[2], int kt) {
+  // Byte shift that realigns a lane's runs: the same on every tile (tile
+  // starts are multiples of 64 keys, so only the row's parity matters).
+  [[maybe_unused]] const uint32_t rel_sh =
+      REL ? (uint32_t)((rrow_b + 2 * (qpos - 3)) & 3) : 0u;
+  // The scores of a bias tile move to the natural-log domain with the bias
+  // added: s*scale + rel[q, h, dist] for 0 <= dist < E, zero outside.
+  // FAST (a whole tile with every dist in [0, E) for every query: no mask,
+  // no band test, every run starts inside its row) costs two byte-aligns
+  // per run and two instructions per score; the checked path handles the
+  // tiles at the diagonal, the run ends and the band edge.
+  [[maybe_unused]] auto bias_apply = [&](f32x16 (&s)[2], int kt, auto fast_c) {
+    constexpr bool fast = decltype(fast_c)::value;
     if constexpr (REL) {
       // dist of the lane's first key for kb = g = 0 (opaque, as above)
       int dq = qpos - kt - 4 * h2;
@@ -509,41 +521,44 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d0 = dq - 32 * kb - 8 * g;
-          const int b = rrow_b + 2 * (d0 - 3);
-          const int b4 = b & ~3;
-          // dwords the load started after the one holding rel[d0-3] (only
-          // when that one lies before the row; 3 or more: every dist of
-          // the run is negative, i.e. masked)
-          const int kd = b4 < 0 ? (-b4) >> 2 : 0;
           const uint32_t x0 = rb[4 * kb + g][0], x1 = rb[4 * kb + g][1],
                          x2 = rb[4 * kb + g][2];
-          const uint32_t y0 = kd == 0 ? x0 : 0u;
-          const uint32_t y1 = kd == 0 ? x1 : (kd == 1 ? x0 : 0u);
-          const uint32_t y2 = kd == 0 ? x2 : (kd == 1 ? x1 : x0);
-          const uint32_t sh = (uint32_t)(b & 3);
-          const uint32_t w0 = __builtin_amdgcn_alignbyte(y1, y0, sh);
-          const uint32_t w1 = __builtin_amdgcn_alignbyte(y2, y1, sh);
+          uint32_t w0, w1;
+          if constexpr (fast) {
+            w0 = __builtin_amdgcn_alignbyte(x1, x0, rel_sh);
+            w1 = __builtin_amdgcn_alignbyte(x2, x1, rel_sh);
+          } else {
+            const int b = rrow_b + 2 * (d0 - 3);
+            const int b4 = b & ~3;
+            // dwords the load started after the one holding rel[d0-3]
+            // (only when that one lies before the row; 3 or more: every
+            // dist of the run is negative, i.e. masked)
+            const int kd = b4 < 0 ? (-b4) >> 2 : 0;
+            const uint32_t y0 = kd == 0 ? x0 : 0u;
+            const uint32_t y1 = kd == 0 ? x1 : (kd == 1 ? x0 : 0u);
+            const uint32_t y2 = kd == 0 ? x2 : (kd == 1 ? x1 : x0);
+            w0 = __builtin_amdgcn_alignbyte(y1, y0, rel_sh);
+            w1 = __builtin_amdgcn_alignbyte(y2, y1, rel_sh);
+          }
           // element 4g + i is key0 + i, dist d0 - i
           const uint32_t hv[4] = {w1 & 0xffff0000u, w1 << 16,
                                   w0 & 0xffff0000u, w0 << 16};
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int dist = d0 - i;
-            const bool band = qok && dist >= 0 && dist < a.rel_extent;
-            const float bias = band ? __builtin_bit_cast(float, hv[i]) : 0.0f;
-            s[kb][4 * g + i] =
-                __builtin_fmaf(s[kb][4 * g + i], a.scale_log2, bias * kLog2e);
+            float bias = __builtin_bit_cast(float, hv[i]);
+            if constexpr (!fast) {
+              const int dist = d0 - i;
+              const bool band = qok && dist >= 0 && dist < a.rel_extent;
+              bias = band ? bias : 0.0f;
+            }
+            s[kb][4 * g + i] = __builtin_fmaf(s[kb][4 * g + i], a.scale, bias);
           }
         }
     }
   };
 
-  // per-element mask (causal, window, run end) and, on tiles within the
-  // bias band, the fused bias
-  auto mask_bias = [&](f32x16 (&s)[2], int kt, bool with_bias) {
-    if constexpr (REL) {
-      if (with_bias) bias_apply(s, kt);
-    }
+  // per-element mask: causal, window, run end
+  auto mask_tile = [&](f32x16 (&s)[2], int kt) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -564,8 +579,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   float l_part = 0.0f;
   // Without a bias the max runs on the raw scores (scale > 0 commutes with
   // max) and each probability is one fma + exp2: p = 2^(s*scale*log2e - m).
-  // (on tiles that carry the fused bias the scores are already in that
-  // domain, and the factor is 1)
+  // (on tiles that carry the fused bias the scores are s*scale + bias,
+  // and the factor is log2e)
 
   // Lazy rescaling: the running max (log2 domain) only moves when the
   // tile's max exceeds it by more than kLazy, so probabilities stay below
@@ -630,8 +645,17 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     // the bias band: some pair of the tile has dist = q - k < E (the
     // smallest dist is pos_lo - (kt + 63))
     const bool with_bias = REL && pos_lo - (kt + kBN - 1) < a.rel_extent;
-    if (with_bias || !full_tile(kt)) mask_bias(s, kt, with_bias);
-    const float sl2 = with_bias ? 1.0f : a.scale_log2;
+    const bool full = full_tile(kt);
+    if constexpr (REL) {
+      if (with_bias) {
+        if (full && pos_hi - kt < a.rel_extent)
+          bias_apply(s, kt, std::true_type{});
+        else
+          bias_apply(s, kt, std::false_type{});
+      }
+    }
+    if (!full) mask_tile(s, kt);
+    const float sl2 = with_bias ? kLog2e : a.scale_log2;
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -1017,6 +1041,7 @@ extern "C" int tmopt_attn_prefill_varlen(
   a.HQ = HQ;
   a.HKV = HKV;
   a.window = window;
+  a.scale = scale;
   a.scale_log2 = scale * kLog2e;
   a.out = (__bf16*)out;
   a.o_st = o_stride_tok;

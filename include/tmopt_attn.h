@@ -314,6 +314,19 @@ int tmopt_attn_prefill_varlen(
     void* out, int64_t o_stride_tok, int64_t o_stride_head, float* lse,
     const int32_t* reject, tmopt_stream_t stream);
 
+/*
+ * The position contract of the reference's fused prefill
+ * (engine/pyengine/kernels/attn_prefill.py:144-186: q_positions and
+ * kv_positions [T] int64, the arange the engine builds, model.py:526-528),
+ * checked on the device without a host synchronisation: writes
+ * *reject = 0 when q_positions[i] - q_positions[0] == i and
+ * kv_positions[i] - q_positions[0] == i for every i < T, else 1 (the
+ * flag tmopt_attn_prefill_varlen takes as `reject`). One work-group.
+ */
+int tmopt_prefill_check_positions(const int64_t* q_positions,
+                                  const int64_t* kv_positions, int64_t T,
+                                  int32_t* reject, tmopt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -101,6 +101,13 @@ def test_invalid_arguments_return_status(tm):
     # zero-size work is a successful no-op
     assert lib.tmopt_kv_write_slots(null, null, 0, 0, 0, 0, null, 0, 4, 128,
                                     null, null, 0, null) == 0
+    # positions check: null pointers and an empty range are refused
+    rc = lib.tmopt_prefill_check_positions(null, p, 8, p, null)
+    assert rc == tm._lib.TMOPT_EINVAL
+    assert b"null pointer" in lib.tmopt_last_error()
+    rc = lib.tmopt_prefill_check_positions(p, p, 0, p, null)
+    assert rc == tm._lib.TMOPT_EINVAL
+    assert b"T must be positive" in lib.tmopt_last_error()
 
 
 def test_python_wrapper_asserts_before_launch(tm):

@@ -118,6 +118,11 @@ def test_attn_prefill_fused_positions(tm, dev):
     assert torch.equal(base, off)
     bad_q = ar.clone()
     bad_q[50] += 1
+    # the device-side check itself (one work-group, flag always written)
+    flags = [int(tm.prefill_check_positions(qp, kp)) for qp, kp in
+             ((ar, ar), (ar + 4096, ar + 4096), (bad_q, ar), (ar, ar + 1),
+              (ar.flip(0), ar.flip(0)))]
+    assert flags == [0, 0, 1, 1, 1]
     for qp, kp in ((bad_q, ar), (ar, ar + 1), (ar.flip(0), ar.flip(0))):
         out = tm.attn_prefill_fused(q, k, v, rel, qp, kp, E)
         torch.cuda.synchronize()

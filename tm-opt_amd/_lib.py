@@ -70,6 +70,8 @@ SIGNATURES = {
         _c_i64, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,
         _c_f32, _c_ptr, _c_i64, _c_i64, _c_i32,
         _c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr]),
+    "tmopt_prefill_check_positions": (_c_i32, [
+        _c_ptr, _c_ptr, _c_i64, _c_ptr, _c_ptr]),
 }
 
 _lock = threading.Lock()

@@ -262,6 +262,25 @@ def decode_paged_noalloc(q, k_pool, v_pool, block_table, ctx_lens, scale,
 # Varlen prefill
 # --------------------------------------------------------------------------
 
+def prefill_check_positions(q_positions, kv_positions, reject=None):
+    """Device-side check of the fused prefill's position contract
+    (attn_prefill.py:144-186): returns (or fills) an int32 [1] flag, 0 when
+    q_positions and kv_positions are both q_positions[0] + arange(T), else
+    1, for prefill_varlen's `reject`. No host synchronisation."""
+    T = q_positions.shape[0]
+    assert q_positions.shape == (T,) and kv_positions.shape == (T,)
+    assert q_positions.dtype == torch.int64
+    assert kv_positions.dtype == torch.int64
+    assert q_positions.is_contiguous() and kv_positions.is_contiguous()
+    assert q_positions.device == kv_positions.device
+    if reject is None:
+        reject = torch.empty(1, dtype=torch.int32, device=q_positions.device)
+    _lib.call("tmopt_prefill_check_positions", _ptr(q_positions),
+              _ptr(kv_positions), T, _ptr(reject),
+              _stream(q_positions.device))
+    return reject
+
+
 def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, max_seqlen=None,
                    prior_lens=None, k_pool=None, v_pool=None,
                    block_table=None, table_wrap=0, rel=None, out=None,

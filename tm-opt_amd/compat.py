@@ -211,13 +211,17 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
     # passes (model.py:526-528). Anything else is rejected: on the device
     # the check feeds the kernel's reject flag (NaN output, no host sync),
     # on the host (CPU positions, or TMOPT_CHECK set) it raises.
-    pos = torch.stack([q_positions, kv_positions.to(q_positions.device)])
-    ar = torch.arange(T, device=pos.device)
-    bad = ((pos - q_positions[:1]) != ar).any()
-    if pos.device.type == "cpu" or os.environ.get("TMOPT_CHECK"):
-        assert not bool(bad), \
+    if (q_positions.device.type == "cpu" or
+            kv_positions.device != q_positions.device or
+            os.environ.get("TMOPT_CHECK")):
+        pos = torch.stack([q_positions, kv_positions.to(q_positions.device)])
+        ar = torch.arange(T, device=pos.device)
+        assert not bool(((pos - q_positions[:1]) != ar).any()), \
             "q_positions and kv_positions must be the same p0 + arange(T)"
-    reject = bad.to(device=dev, dtype=torch.int32).reshape(1)
+        reject = None
+    else:
+        reject = attn.prefill_check_positions(q_positions.contiguous(),
+                                              kv_positions.contiguous())
     qp = _packed(q, B, T, H, D)
     rt = rel.transpose(1, 2)                     # [B, T, H, E]
     if not (B == 1 or rt.stride(0) == T * rt.stride(1)):

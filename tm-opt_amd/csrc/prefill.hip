@@ -919,10 +919,40 @@ void launch(PrefillArgs a, int src, int S, int max_seqlen, hipStream_t st) {
     launch_src<REP, false>(a, src, grid, lds, st);
 }
 
+// One work-group: *reject = 1 unless q_pos[i] - q_pos[0] == i and
+// kv_pos[i] - q_pos[0] == i for every i < T (always written, so the flag
+// needs no clearing).
+__global__ __launch_bounds__(1024) void positions_check_kernel(
+    const int64_t* __restrict__ q_pos, const int64_t* __restrict__ kv_pos,
+    int64_t T, int32_t* __restrict__ reject) {
+  const int64_t p0 = q_pos[0];
+  int bad = 0;
+  for (int64_t i = threadIdx.x; i < T; i += blockDim.x)
+    bad |= (q_pos[i] - p0 != i) | (kv_pos[i] - p0 != i);
+  bad = __syncthreads_or(bad);
+  if (threadIdx.x == 0) reject[0] = bad ? 1 : 0;
+}
+
 }  // namespace
 }  // namespace tmopt
 
 using namespace tmopt;
+
+extern "C" int tmopt_prefill_check_positions(const int64_t* q_positions,
+                                             const int64_t* kv_positions,
+                                             int64_t T, int32_t* reject,
+                                             tmopt_stream_t stream) {
+  clear_error();
+  TMOPT_REQUIRE(q_positions && kv_positions && reject, TMOPT_EINVAL,
+                "prefill_check_positions: null pointer");
+  TMOPT_REQUIRE(T > 0, TMOPT_EINVAL,
+                "prefill_check_positions: T must be positive (got %lld)",
+                (long long)T);
+  hipLaunchKernelGGL(positions_check_kernel, dim3(1), dim3(1024), 0,
+                     (hipStream_t)stream, q_positions, kv_positions, T,
+                     reject);
+  return check_launch("prefill_check_positions");
+}
 
 extern "C" int tmopt_attn_prefill_varlen(
     const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k,

@@ -14,11 +14,17 @@ output layouts, and run the gfx950 kernels of this package:
     are turned back into a block table: rows of one page are consecutive,
     so page i of row b is flat[b, 16 i] // 16;
   * the padded [B, H, T, D] prefill batch becomes B packed runs of T tokens
-    (cu_seqlens = 0, T, 2T, ...), read in place when the strides allow and
-    copied to the packed layout otherwise (e.g. channel-major K/V).
+    (cu_seqlens = 0, T, 2T, ...), read in place when the strides allow;
+    channel-major K/V (the sconv output) are packed on chip by the paged
+    write's transposing kernel, other layouts copied;
+  * the prefill's position contract is checked on the device
+    (tmopt_prefill_check_positions feeds the kernel's reject flag).
 
-No host synchronisation: every helper tensor is built with device ops, so
-the adapters can run inside hipGraph capture.
+No host synchronisation in attn_swa, attn_global and attn_prefill_fused
+without caches: every helper tensor is built with device ops (or, once
+per shape, copied from pinned memory), so they can run inside hipGraph
+capture. The cache-populating paths take the rows' lengths from the host
+cache objects, as the reference's appends do.
 """
 import os
 
@@ -120,7 +126,7 @@ def _pack_channel_major(k, v, B, T, H, D):
             m[b, 2] = T
             m[b, 3:] = torch.clamp(torch.arange(w) + (b * T) // PAGE,
                                    max=P - 1)
-        meta = _PACK_META[key] = m.to(dev)
+        meta = _PACK_META[key] = _to_device(m.tolist(), dev)
     kp = torch.empty((P, PAGE, H, D), dtype=k.dtype, device=dev)
     vp = torch.empty_like(kp)
     for b in range(B):
@@ -128,6 +134,16 @@ def _pack_channel_major(k, v, B, T, H, D):
                             meta[b, 0:1], kp, vp, cu_seqlens=meta[b, 1:3],
                             max_seqlen=T)
     return (kp.view(P * PAGE, H, D)[:B * T], vp.view(P * PAGE, H, D)[:B * T])
+
+
+def _to_device(rows, dev):
+    """int32 rows (a host list) on the device through pinned memory: the
+    copy is queued on the stream instead of synchronising it (the caching
+    host allocator keeps the staging buffer until the copy has run)."""
+    t = torch.tensor(rows, dtype=torch.int32)
+    if dev.type != "cuda":
+        return t.to(dev)
+    return t.pin_memory().to(dev, non_blocking=True)
 
 
 def _append_rows(k, v, caches, lens):
@@ -141,10 +157,10 @@ def _append_rows(k, v, caches, lens):
     B = k.shape[0]
     dev = k.device
     rows = []
-    # every row's start position and run bounds in one host-to-device copy
-    # (a copy from pageable memory synchronises the stream)
-    meta = torch.tensor([[int(caches[i].n), 0, int(lens[i])]
-                         for i in range(B)], dtype=torch.int32).to(dev)
+    # every row's start position and run bounds in one host-to-device copy,
+    # from pinned memory so that it does not synchronise the stream
+    meta = _to_device([[int(caches[i].n), 0, int(lens[i])]
+                       for i in range(B)], dev)
     for i in range(B):
         c = caches[i]
         n0, T = int(c.n), int(lens[i])
@@ -156,7 +172,7 @@ def _append_rows(k, v, caches, lens):
             if getattr(c, "table_dev_row", None) is not None:
                 row = c.table_dev_row.to(torch.int32)[None]
             else:                                # a PagedKV with its own pool
-                row = torch.tensor([c.table], dtype=torch.int32, device=dev)
+                row = _to_device([c.table], dev)
             attn.kv_write_paged(kt, vt, row, start, c.kp, c.vp,
                                 cu_seqlens=cu, max_seqlen=T)
             rows.append(row)

@@ -290,8 +290,7 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
 
 def _chunk_cu(q, cu_seqlens):
     if cu_seqlens is None:
-        return torch.tensor([0, q.shape[0]], dtype=torch.int32,
-                            device=q.device)
+        return _to_device([0, q.shape[0]], q.device)
     assert cu_seqlens.dtype == torch.int32
     return cu_seqlens
 
@@ -375,8 +374,8 @@ def prefill_chunk_state(q, k, v, rel, cache):
     T, H, D = q.shape
     dev = q.device
     n = int(cache.n)
-    prior = torch.tensor([n], dtype=torch.int32, device=dev)
-    cu = torch.tensor([0, T], dtype=torch.int32, device=dev)
+    meta = _to_device([n, 0, T], dev)            # prior, cu_seqlens
+    prior, cu = meta[0:1], meta[1:3]
     if hasattr(cache, "kp"):
         ps = cache.page_size
         assert ps == PAGE
@@ -384,7 +383,7 @@ def prefill_chunk_state(q, k, v, rel, cache):
         if getattr(cache, "table_dev_row", None) is not None:
             table = cache.table_dev_row.to(torch.int32)[None].contiguous()
         else:                                    # a PagedKV with its own pool
-            table = torch.tensor([cache.table], dtype=torch.int32, device=dev)
+            table = _to_device([cache.table], dev)
         kp, vp, wrap, window = cache.kp, cache.vp, 0, 0
     else:
         W = cache.k.shape[0]

@@ -331,9 +331,11 @@ class AttnGraphRunner:
             self._capture(L_pad)
         self.hiwater = L_pad
         dead = self.MB - B
-        self.pos_buf.copy_(torch.tensor(list(pos) + [0] * dead,
-                                        dtype=torch.int64))
-        self.slots_buf.copy_(torch.tensor(list(slots) + [self.scratch] * dead,
-                                          dtype=torch.int64))
+        # staged through pinned memory: queued on the stream, no host sync
+        host = torch.tensor([list(pos) + [0] * dead,
+                             list(slots) + [self.scratch] * dead],
+                            dtype=torch.int64).pin_memory()
+        self.pos_buf.copy_(host[0], non_blocking=True)
+        self.slots_buf.copy_(host[1], non_blocking=True)
         self.programs[L_pad].replay()
         return L_pad

@@ -131,6 +131,20 @@ def test_attn_prefill_fused_positions(tm, dev):
         tm.attn_prefill_fused(q, k, v, rel, bad_q.cpu(), ar.cpu(), E)
 
 
+def test_positions_check_lengths(tm, dev):
+    """The one-work-group position check strides over T: a mismatch at the
+    last index is found for T below, at and past the work-group size, and
+    T = 1 (only the offset) passes."""
+    for T in (1, 1024, 1025, 5000):
+        ar = torch.arange(T, device=dev) + 7
+        assert int(tm.prefill_check_positions(ar, ar)) == 0
+        if T > 1:
+            for which in ("q", "kv"):
+                q, k = ar.clone(), ar.clone()
+                (q if which == "q" else k)[-1] += 1
+                assert int(tm.prefill_check_positions(q, k)) == 1, (T, which)
+
+
 @pytest.mark.parametrize("kind", ["global", "swa"])
 def test_attn_prefill_fused_populates_caches(tm, dev, kind):
     """attn_prefill_fused given the rows' caches (the engine's

@@ -99,8 +99,9 @@ def _packed(x, B, T, H, D):
 
 
 # per (B, T, device): the identity page tables of _pack_channel_major, built
-# once (a host-to-device copy from pageable memory synchronises the stream)
+# once per shape; the oldest entries go first past _PACK_META_MAX shapes
 _PACK_META = {}
+_PACK_META_MAX = 64
 
 
 def _pack_channel_major(k, v, B, T, H, D):
@@ -126,6 +127,8 @@ def _pack_channel_major(k, v, B, T, H, D):
             m[b, 2] = T
             m[b, 3:] = torch.clamp(torch.arange(w) + (b * T) // PAGE,
                                    max=P - 1)
+        if len(_PACK_META) >= _PACK_META_MAX:
+            _PACK_META.pop(next(iter(_PACK_META)))
         meta = _PACK_META[key] = _to_device(m.tolist(), dev)
     kp = torch.empty((P, PAGE, H, D), dtype=k.dtype, device=dev)
     vp = torch.empty_like(kp)

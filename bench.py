@@ -103,10 +103,12 @@ def bench_decode(tm, wl, make, steps, warmup, n_sets=2, min_pages=8,
     }
 
 
-def bench_prefill(tm, wl, window, steps, warmup, n_sets=2):
+def bench_prefill(tm, wl, window, steps, warmup, n_sets=2, make=None):
     """Config 4: varlen causal prefill, 8 runs T ~ U[512, 8192], once global
-    and once with window 4096. FLOPs = 4 * D * HQ * visible (q, k) pairs."""
-    sets = [wl.config4(window=window, device="cuda") for _ in range(n_sets)]
+    and once with window 4096 (or `make`'s runs, e.g. config4_long). FLOPs =
+    4 * D * HQ * visible (q, k) pairs."""
+    make = make or wl.config4
+    sets = [make(window=window, device="cuda") for _ in range(n_sets)]
     c0 = sets[0]
     total = c0.q.shape[0]
     bufs = {id(c): (torch.empty_like(c.q),
@@ -695,6 +697,15 @@ def main():
                   f" us {r['tflops_events']:.0f} TFLOP/s", file=sys.stderr,
                   flush=True)
             extra["C4_prefill_" + ("global" if win == 0 else f"swa{win}")] = r
+        for win in (0, 4096):
+            r = bench_prefill(tm, wl, win, max(5, args.steps // 5),
+                              max(20, args.warmup // 5), make=wl.config4_long)
+            print(f"[bench] 4x8192 prefill w={win} "
+                  f"{r['us_per_launch_events']:.0f} us "
+                  f"{r['tflops_events']:.0f} TFLOP/s", file=sys.stderr,
+                  flush=True)
+            extra["C4_long_prefill_" + ("global" if win == 0 else
+                                        f"swa{win}")] = r
         r = bench_kv_write(tm, wl, args.steps, xw)
         print(f"[bench] C4 kv write {r['us_per_launch_events']:.1f} us "
               f"{r['gbs_events']:.0f} GB/s", file=sys.stderr, flush=True)

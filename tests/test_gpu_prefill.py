@@ -172,12 +172,15 @@ def test_determinism(tm, dev):
     assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
 
 
-@pytest.mark.parametrize("window", [0, 4096])
-def test_config4_sampled_rows(tm, dev, window):
-    """BASELINE config 4 at full size; the oracle checks 48 sampled query
-    rows per sequence (first, last, around the 4096 window edge, random)."""
+@pytest.mark.parametrize("make,window", [("config4", 0), ("config4", 4096),
+                                         ("config4_long", 4096)])
+def test_config4_sampled_rows(tm, dev, make, window):
+    """BASELINE config 4 at full size, and its head config on 4 runs of 8192
+    tokens with window 4096 (half of each run's queries see a full window);
+    the oracle checks 48 sampled query rows per sequence (first, last,
+    around the 4096 window edge, random)."""
     wl = _wl()
-    case = wl.config4(window=window)
+    case = getattr(wl, make)(window=window)
     out, lse = _gpu(tm, case, dev)
     assert torch.isfinite(out.float()).all()
     g = torch.Generator().manual_seed(99)

@@ -92,3 +92,34 @@ def test_decode_step_graph_replays(tm, dev):
             p = int(ctx[b]) - 1
             pg = int(ly["block_table"][b, p // 16])
             assert torch.equal(ly["k_pool"][pg, p % 16], dg.k_new[0, b])
+
+
+def test_prefill_fused_first_call_in_capture(tm, dev):
+    """attn_prefill_fused with channel-major K/V and the fused bias,
+    captured in a hipGraph on its first call for the shape (the on-chip
+    packing's identity table and the position check are then built inside
+    the capture): every replay, with eager work and a synchronisation
+    between replays, equals the eager call bitwise."""
+    compat = import_module("tm-opt_amd.compat")
+    g = torch.Generator().manual_seed(23)
+    B, T, D, hq, hk, W = 2, 136, 128, 32, 4, 64
+    q = torch.randn((B, T, hq, D), generator=g).to(torch.bfloat16).to(dev)
+    kc = torch.randn((B, hk, D, T), generator=g).to(torch.bfloat16).to(dev)
+    vc = torch.randn((B, hk, D, T), generator=g).to(torch.bfloat16).to(dev)
+    rel = (torch.randn((B, T, hq, W), generator=g) * 0.5).to(
+        torch.bfloat16).to(dev)
+    args = (q.transpose(1, 2), kc.transpose(2, 3), vc.transpose(2, 3),
+            rel.transpose(1, 2), torch.arange(T, device=dev),
+            torch.arange(T, device=dev), W)
+    eager = tm.attn_prefill_fused(*args)
+    torch.cuda.synchronize()
+    compat._PACK_META.clear()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = tm.attn_prefill_fused(*args)
+    for _ in range(3):
+        graph.replay()
+        noise = torch.randn((1 << 20,), device=dev) * 2.0   # eager work
+        torch.cuda.synchronize()
+        del noise
+        assert torch.equal(out, eager)

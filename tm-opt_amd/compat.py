@@ -20,11 +20,12 @@ output layouts, and run the gfx950 kernels of this package:
   * the prefill's position contract is checked on the device
     (tmopt_prefill_check_positions feeds the kernel's reject flag).
 
-No host synchronisation in attn_swa, attn_global and attn_prefill_fused
-without caches: every helper tensor is built with device ops (or, once
-per shape, copied from pinned memory), so they can run inside hipGraph
-capture. The cache-populating paths take the rows' lengths from the host
-cache objects, as the reference's appends do.
+No host synchronisation in attn_swa, attn_global, attn_prefill_fused
+without caches and the pooled chunk adapters: every helper tensor is built
+with device ops, so they can run inside hipGraph capture. The
+cache-populating paths take the rows' lengths from the host cache
+objects, as the reference's appends do (their small metadata tensors go
+through pinned memory, without a stream synchronisation).
 """
 import os
 
@@ -121,15 +122,18 @@ def _pack_channel_major(k, v, B, T, H, D):
     key = (B, T, dev)
     meta = _PACK_META.get(key)
     if meta is None:
-        m = torch.zeros((B, 3 + w), dtype=torch.int32)
-        for b in range(B):
-            m[b, 0] = (b * T) % PAGE
-            m[b, 2] = T
-            m[b, 3:] = torch.clamp(torch.arange(w) + (b * T) // PAGE,
-                                   max=P - 1)
+        # built with device ops (no host copy, so also legal in a capture)
+        start = torch.arange(B, dtype=torch.int32, device=dev) * T
+        meta = torch.empty((B, 3 + w), dtype=torch.int32, device=dev)
+        meta[:, 0] = start % PAGE
+        meta[:, 1] = 0
+        meta[:, 2] = T
+        meta[:, 3:] = torch.clamp(
+            torch.arange(w, dtype=torch.int32, device=dev)[None] +
+            (start // PAGE)[:, None], max=P - 1)
         if len(_PACK_META) >= _PACK_META_MAX:
             _PACK_META.pop(next(iter(_PACK_META)))
-        meta = _PACK_META[key] = _to_device(m.tolist(), dev)
+        _PACK_META[key] = meta
     kp = torch.empty((P, PAGE, H, D), dtype=k.dtype, device=dev)
     vp = torch.empty_like(kp)
     for b in range(B):
@@ -293,7 +297,10 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
 
 def _chunk_cu(q, cu_seqlens):
     if cu_seqlens is None:
-        return _to_device([0, q.shape[0]], q.device)
+        cu = torch.full((2,), q.shape[0], dtype=torch.int32,
+                        device=q.device)
+        cu[0] = 0
+        return cu
     assert cu_seqlens.dtype == torch.int32
     return cu_seqlens
 

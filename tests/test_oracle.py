@@ -483,3 +483,4 @@ def test_prefill_paged_zero_query_closed_form(c):
             rows.append(c["v"][c["cu"][i] + p - p0, 0])
     want = torch.stack(rows).float().mean(0)
     assert (out[c["cu"][i] + T - 1, 0] - want).abs().max() < 1e-5
+

@@ -105,6 +105,26 @@ _PACK_META = {}
 _PACK_META_MAX = 64
 
 
+def _pack_meta(B, T, dev):
+    """Per row b of a [B*T]-row packed buffer seen as 16-row pages: [start
+    slot, 0, T, page ids...] int32 [B, 3 + w], so that position start + i
+    of row b lands in packed row b*T + i under the page rule
+    table[p // 16] * 16 + p % 16 (entries past the buffer clamp to its last
+    page and are never reached). Built with device ops: no host copy, so it
+    is also legal inside a graph capture."""
+    P = (B * T + PAGE - 1) // PAGE
+    w = (T + PAGE - 1) // PAGE + 1
+    start = torch.arange(B, dtype=torch.int32, device=dev) * T
+    meta = torch.empty((B, 3 + w), dtype=torch.int32, device=dev)
+    meta[:, 0] = start % PAGE
+    meta[:, 1] = 0
+    meta[:, 2] = T
+    meta[:, 3:] = torch.clamp(
+        torch.arange(w, dtype=torch.int32, device=dev)[None] +
+        (start // PAGE)[:, None], max=P - 1)
+    return meta
+
+
 def _pack_channel_major(k, v, B, T, H, D):
     """Channel-major [B, H, T, D] K/V views (the sconv output: tokens
     contiguous) -> packed [B*T, H, D] rows, transposed on chip by the paged
@@ -118,19 +138,10 @@ def _pack_channel_major(k, v, B, T, H, D):
         return None
     dev = k.device
     P = (B * T + PAGE - 1) // PAGE
-    w = (T + PAGE - 1) // PAGE + 1
     key = (B, T, dev)
     meta = _PACK_META.get(key)
     if meta is None:
-        # built with device ops (no host copy, so also legal in a capture)
-        start = torch.arange(B, dtype=torch.int32, device=dev) * T
-        meta = torch.empty((B, 3 + w), dtype=torch.int32, device=dev)
-        meta[:, 0] = start % PAGE
-        meta[:, 1] = 0
-        meta[:, 2] = T
-        meta[:, 3:] = torch.clamp(
-            torch.arange(w, dtype=torch.int32, device=dev)[None] +
-            (start // PAGE)[:, None], max=P - 1)
+        meta = _pack_meta(B, T, dev)
         if len(_PACK_META) >= _PACK_META_MAX:
             _PACK_META.pop(next(iter(_PACK_META)))
         _PACK_META[key] = meta

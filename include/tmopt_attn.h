@@ -116,6 +116,29 @@ int tmopt_kv_write_paged(const void* k, const void* v, int64_t k_stride_tok,
                          void* k_pool, void* v_pool, int64_t num_pages,
                          tmopt_stream_t stream);
 
+/*
+ * The prefill's cache population for a whole batch in one launch. Replaces
+ * the engine's per-row loop (engine/pyengine/model.py:507-512:
+ * st.cache.append(kn[i, :lens[i]], vv[i, :lens[i]]) for each row i, i.e.
+ * PagedKV.append / RingKV.append, kv.py:193-205, :89-103): row r's tokens
+ * t < lens[r] are k + r * k_stride_row + t * k_stride_tok + h *
+ * k_stride_head + d * k_stride_dim (v likewise), written at logical
+ * positions start_pos[r] + t through block-table row r, with every rule of
+ * tmopt_kv_write_paged (page rule, ring wrap and drop, row-width bound,
+ * skipped out-of-pool entries, token-major or channel-major rows). Row
+ * strides are multiples of 8 elements; max_len >= every lens[r].
+ */
+int tmopt_kv_append_rows(const void* k, const void* v, int64_t k_stride_row,
+                         int64_t k_stride_tok, int64_t k_stride_head,
+                         int64_t k_stride_dim, int64_t v_stride_row,
+                         int64_t v_stride_tok, int64_t v_stride_head,
+                         int64_t v_stride_dim, const int32_t* lens,
+                         const int32_t* start_pos, int num_rows, int max_len,
+                         const int32_t* block_table, int64_t bt_stride,
+                         int table_wrap, int page_size, int HKV, int D,
+                         void* k_pool, void* v_pool, int64_t num_pages,
+                         tmopt_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Paged decode attention (split-KV + LSE combine)                          */
 /* ------------------------------------------------------------------------ */

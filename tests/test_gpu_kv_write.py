@@ -419,3 +419,53 @@ def test_write_paged_channel_major_engine_views(tm, dev):
     torch.cuda.synchronize()
     assert np.array_equal(kv_ref.as_u16(kd), want_k)
     assert np.array_equal(kv_ref.as_u16(vd), want_v)
+
+
+@pytest.mark.parametrize("layout", ["token", "channel"])
+@pytest.mark.parametrize("wrap", [0, 5])
+def test_append_rows_batch(tm, dev, layout, wrap):
+    """tmopt_kv_append_rows: B rows of a padded [B, T, H, D] batch (the
+    prefill's st.cache.append(kn[i, :lens[i]], ...) loop, model.py:507-512)
+    in one launch: ragged lengths including 0 and the full T, starts off the
+    page grid, token-major and channel-major sources, a ring table with
+    RingKV's drop rule; bit-exact against the oracle's per-row appends."""
+    g = torch.Generator().manual_seed(61 + wrap)
+    B, T, H, D = 5, 136, 4, 128
+    lens = [136, 0, 57, 1, 100]
+    start = [0, 5, 19, 200, 33]
+    k = _bf16((B, T, H, D), g)
+    v = _bf16((B, T, H, D), g)
+    per = [wrap if wrap else (s + n + 15) // 16 + 1 for s, n in zip(start, lens)]
+    width = max(per)
+    P = sum(per) + 2
+    perm = torch.randperm(P, generator=g).to(torch.int32)
+    table = torch.full((B, width), -1, dtype=torch.int32)
+    off = 0
+    for i, n in enumerate(per):
+        table[i, :n] = perm[off:off + n]
+        off += n
+    kp = _bf16((P, 16, H, D), g)
+    vp = _bf16((P, 16, H, D), g)
+    # the oracle: the rows' first lens[i] tokens as packed runs
+    rows_k = torch.cat([k[i, :lens[i]] for i in range(B)])
+    rows_v = torch.cat([v[i, :lens[i]] for i in range(B)])
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    want_k = kv_ref.write_paged(kv_ref.as_u16(kp).copy(), kv_ref.as_u16(rows_k),
+                                cu, start, table.numpy(), 16, wrap)
+    want_v = kv_ref.write_paged(kv_ref.as_u16(vp).copy(), kv_ref.as_u16(rows_v),
+                                cu, start, table.numpy(), 16, wrap)
+    if layout == "token":
+        kd, vd = k.to(dev), v.to(dev)
+    else:
+        # channel-major per row: [B, H, D, T] storage viewed as [B, T, H, D]
+        kd = k.permute(0, 2, 3, 1).contiguous().to(dev).permute(0, 3, 1, 2)
+        vd = v.permute(0, 2, 3, 1).contiguous().to(dev).permute(0, 3, 1, 2)
+        assert kd.stride(1) == 1 and kd.stride(3) == T
+    kpd, vpd = kp.to(dev), vp.to(dev)
+    tm.kv_append_rows(kd, vd, torch.tensor(lens, dtype=torch.int32,
+                                           device=dev),
+                      torch.tensor(start, dtype=torch.int32, device=dev),
+                      table.to(dev), kpd, vpd, table_wrap=wrap)
+    torch.cuda.synchronize()
+    assert np.array_equal(kv_ref.as_u16(kpd), want_k)
+    assert np.array_equal(kv_ref.as_u16(vpd), want_v)

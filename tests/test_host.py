@@ -13,14 +13,13 @@ def test_pack_meta_is_an_identity_layout(B, T):
     row b is packed row b*T + i for every i < T, and no table entry read for
     those positions leaves the buffer."""
     compat = import_module("tm-opt_amd.compat")
-    meta = compat._pack_meta(B, T, "cpu")
+    start, lens, table = compat._pack_meta(B, T, "cpu")
     P = (B * T + 15) // 16
+    assert table.is_contiguous() and table.shape[0] == B
+    assert torch.equal(lens, torch.full((B,), T, dtype=torch.int32))
     for b in range(B):
-        start, lo, n = (int(x) for x in meta[b, :3])
-        assert (lo, n) == (0, T)
-        pos = start + torch.arange(T)
-        table = meta[b, 3:]
-        assert int(pos[-1]) // 16 < table.numel()
-        rows = table[pos // 16].long() * 16 + pos % 16
+        pos = int(start[b]) + torch.arange(T)
+        assert int(pos[-1]) // 16 < table.shape[1]
+        rows = table[b][pos // 16].long() * 16 + pos % 16
         assert torch.equal(rows, b * T + torch.arange(T))
-        assert int(table[pos // 16].max()) < P
+        assert int(table[b][pos // 16].max()) < P

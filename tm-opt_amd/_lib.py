@@ -49,6 +49,10 @@ SIGNATURES = {
         _c_ptr, _c_ptr,
         _c_i32, _c_i32, _c_ptr, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,
         _c_ptr, _c_ptr, _c_i64, _c_ptr]),
+    "tmopt_kv_append_rows": (_c_i32, [
+        _c_ptr, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64,
+        _c_i64, _c_i64, _c_ptr, _c_ptr, _c_i32, _c_i32, _c_ptr, _c_i64,
+        _c_i32, _c_i32, _c_i32, _c_i32, _c_ptr, _c_ptr, _c_i64, _c_ptr]),
     "tmopt_attn_decode_default_workgroups": (_c_i32, [_c_i32]),
     "tmopt_attn_decode_workspace_size": (_c_size, [
         _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),

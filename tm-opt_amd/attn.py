@@ -105,6 +105,40 @@ def kv_write_paged(k, v, block_table, start_pos, k_pool, v_pool,
               _ptr(k_pool), _ptr(v_pool), P, _stream(k.device))
 
 
+def kv_append_rows(k, v, lens, start_pos, block_table, k_pool, v_pool,
+                   max_len=None, table_wrap=0):
+    """The prefill's cache population for a batch in one launch
+    (model.py:507-512: st.cache.append(kn[i, :lens[i]], vv[i, :lens[i]])
+    for every row i): k, v [B, T, HKV, D] bf16 views, token-major (head_dim
+    contiguous) or channel-major (tokens contiguous), row stride a multiple
+    of 8; lens / start_pos [B] int32 (device); block_table [B, width] int32
+    with whole rows; pools [num_pages, page_size, HKV, D]. Row i's first
+    lens[i] tokens land at positions start_pos[i].. through table row i, with
+    every rule of kv_write_paged (kv.py:89-103, :193-205)."""
+    B, T, HKV, D = k.shape
+    assert v.shape == k.shape
+    for x, name in ((k, "k"), (v, "v")):
+        assert x.dtype == torch.bfloat16, f"{name} must be bf16"
+        assert x.stride(-1) == 1 or x.stride(1) == 1, \
+            f"{name}: head_dim or tokens must be contiguous"
+    assert lens.dtype == torch.int32 and lens.shape == (B,)
+    assert start_pos.dtype == torch.int32 and start_pos.shape == (B,)
+    assert block_table.dtype == torch.int32 and block_table.dim() == 2
+    assert block_table.shape[0] >= B and block_table.stride(1) == 1
+    assert block_table.stride(0) == block_table.shape[1] or B <= 1, \
+        "block-table rows must be whole (the row width is the stride)"
+    assert k_pool.is_contiguous() and v_pool.is_contiguous()
+    assert k_pool.shape == v_pool.shape and k_pool.dim() == 4
+    P, page_size = k_pool.shape[0], k_pool.shape[1]
+    assert tuple(k_pool.shape[2:]) == (HKV, D)
+    _lib.call("tmopt_kv_append_rows", _ptr(k), _ptr(v), k.stride(0),
+              k.stride(1), k.stride(2), k.stride(3), v.stride(0), v.stride(1),
+              v.stride(2), v.stride(3), _ptr(lens), _ptr(start_pos), B,
+              int(T if max_len is None else max_len), _ptr(block_table),
+              block_table.stride(0), int(table_wrap), page_size, HKV, D,
+              _ptr(k_pool), _ptr(v_pool), P, _stream(k.device))
+
+
 # --------------------------------------------------------------------------
 # Paged decode
 # --------------------------------------------------------------------------

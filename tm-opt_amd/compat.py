@@ -106,8 +106,8 @@ _PACK_META_MAX = 64
 
 
 def _pack_meta(B, T, dev):
-    """Per row b of a [B*T]-row packed buffer seen as 16-row pages: [start
-    slot, 0, T, page ids...] int32 [B, 3 + w], so that position start + i
+    """Identity tables of a [B*T]-row packed buffer seen as 16-row pages:
+    (start [B], lens [B], table [B, w]) int32, so that position start[b] + i
     of row b lands in packed row b*T + i under the page rule
     table[p // 16] * 16 + p % 16 (entries past the buffer clamp to its last
     page and are never reached). Built with device ops: no host copy, so it
@@ -115,26 +115,24 @@ def _pack_meta(B, T, dev):
     P = (B * T + PAGE - 1) // PAGE
     w = (T + PAGE - 1) // PAGE + 1
     start = torch.arange(B, dtype=torch.int32, device=dev) * T
-    meta = torch.empty((B, 3 + w), dtype=torch.int32, device=dev)
-    meta[:, 0] = start % PAGE
-    meta[:, 1] = 0
-    meta[:, 2] = T
-    meta[:, 3:] = torch.clamp(
+    table = torch.clamp(
         torch.arange(w, dtype=torch.int32, device=dev)[None] +
-        (start // PAGE)[:, None], max=P - 1)
-    return meta
+        (start // PAGE)[:, None], max=P - 1).contiguous()
+    lens = torch.full((B,), T, dtype=torch.int32, device=dev)
+    return start % PAGE, lens, table
 
 
 def _pack_channel_major(k, v, B, T, H, D):
     """Channel-major [B, H, T, D] K/V views (the sconv output: tokens
-    contiguous) -> packed [B*T, H, D] rows, transposed on chip by the paged
-    write over an identity table: the packed buffer is a pool of 16-row
-    pages, row b starts at page (b*T)//16, slot (b*T)%16. None when the
-    layout is outside what that kernel reads (then the caller copies)."""
-    views = [x[b].transpose(0, 1) for x in (k, v) for b in range(B)]
+    contiguous) -> packed [B*T, H, D] rows, transposed on chip by one
+    batched append over identity tables: the packed buffer is a pool of
+    16-row pages, row b starts at page (b*T)//16, slot (b*T)%16. None when
+    the layout is outside what that kernel reads (then the caller copies)."""
+    kt, vt = k.transpose(1, 2), v.transpose(1, 2)       # [B, T, H, D]
     if not (T % 8 == 0 and D == attn.HEAD_DIM and
-            all(attn._channel_major(x) and x.data_ptr() % 16 == 0
-                for x in views)):
+            all(x.stride(1) == 1 and x.stride(3) != 1 and
+                x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
+                for x in (kt, vt))):
         return None
     dev = k.device
     P = (B * T + PAGE - 1) // PAGE
@@ -145,12 +143,10 @@ def _pack_channel_major(k, v, B, T, H, D):
         if len(_PACK_META) >= _PACK_META_MAX:
             _PACK_META.pop(next(iter(_PACK_META)))
         _PACK_META[key] = meta
+    start, lens, table = meta
     kp = torch.empty((P, PAGE, H, D), dtype=k.dtype, device=dev)
     vp = torch.empty_like(kp)
-    for b in range(B):
-        attn.kv_write_paged(views[b], views[B + b], meta[b:b + 1, 3:],
-                            meta[b, 0:1], kp, vp, cu_seqlens=meta[b, 1:3],
-                            max_seqlen=T)
+    attn.kv_append_rows(kt, vt, lens, start, table, kp, vp, max_len=T)
     return (kp.view(P * PAGE, H, D)[:B * T], vp.view(P * PAGE, H, D)[:B * T])
 
 
@@ -170,44 +166,65 @@ def _append_rows(k, v, caches, lens):
     row's K/V [lens[i], HK, D] is appended to its cache straight from the
     (channel-major or token-major) views, pages allocated on the host as
     PagedKV.append does (kv.py:196-198), ring rows as RingKV.append keeps
-    them (kv.py:89-103); cache.n advances. Returns the int32 block-table
-    rows of page caches ([B, num_pages]) or None for rings."""
+    them (kv.py:89-103); cache.n advances. Page caches that share one pool
+    (GlobalPool rows) take one batched launch for all rows; rings and
+    caches with pools of their own one launch each. Returns the int32
+    block-table rows of page caches ([B, num_pages]) or None for rings."""
     B = k.shape[0]
     dev = k.device
-    rows = []
-    # every row's start position and run bounds in one host-to-device copy,
-    # from pinned memory so that it does not synchronise the stream
-    meta = _to_device([[int(caches[i].n), 0, int(lens[i])]
-                       for i in range(B)], dev)
-    for i in range(B):
-        c = caches[i]
-        n0, T = int(c.n), int(lens[i])
-        kt = k[i].transpose(0, 1)[:T]            # [T, HK, D] view
-        vt = v[i].transpose(0, 1)[:T]
-        start, cu = meta[i, 0:1], meta[i, 1:3]
+    n0 = [int(c.n) for c in caches]
+    T = [int(x) for x in lens]
+    # every row's start position, length and [0, length] run bounds in one
+    # host-to-device copy, from pinned memory so that it does not
+    # synchronise the stream
+    flat = n0 + T + [x for t in T for x in (0, t)]
+    meta = _to_device(flat, dev)
+    start, lens_d = meta[:B], meta[B:2 * B]
+    paged = all(hasattr(c, "kp") for c in caches)
+    for i, c in enumerate(caches):
         if hasattr(c, "kp"):
-            c.ensure_pages((n0 + T - 1) // c.page_size)
-            if getattr(c, "table_dev_row", None) is not None:
-                row = c.table_dev_row.to(torch.int32)[None]
-            else:                                # a PagedKV with its own pool
-                row = _to_device([c.table], dev)
-            attn.kv_write_paged(kt, vt, row, start, c.kp, c.vp,
-                                cu_seqlens=cu, max_seqlen=T)
-            rows.append(row)
-        else:
-            W = c.k.shape[0]
-            per = W // PAGE
-            ring = torch.arange(per, dtype=torch.int32, device=dev)[None]
-            attn.kv_write_paged(kt, vt, ring, start,
-                                c.k.view(per, PAGE, *c.k.shape[1:]),
-                                c.v.view(per, PAGE, *c.v.shape[1:]),
-                                cu_seqlens=cu, max_seqlen=T, table_wrap=per)
-        c.n = n0 + T
-    if not rows:
-        return None
-    width = max(r.shape[1] for r in rows)
-    return torch.cat([torch.nn.functional.pad(r, (0, width - r.shape[1]),
-                                              value=-1) for r in rows])
+            c.ensure_pages((n0[i] + T[i] - 1) // c.page_size)
+    rows = None
+    if paged:
+        if all(getattr(c, "table_dev_row", None) is not None for c in caches):
+            rows = [c.table_dev_row.to(torch.int32) for c in caches]
+            width = max(r.shape[0] for r in rows)
+            rows = torch.stack([torch.nn.functional.pad(
+                r, (0, width - r.shape[0]), value=-1) for r in rows])
+        else:                                    # PagedKV with host tables
+            width = max(len(c.table) for c in caches)
+            rows = _to_device([list(c.table) + [-1] * (width - len(c.table))
+                               for c in caches], dev)
+    shared = paged and all(c.kp is caches[0].kp and c.vp is caches[0].vp
+                           for c in caches)
+    if shared:
+        c0 = caches[0]
+        attn.kv_append_rows(k.transpose(1, 2), v.transpose(1, 2), lens_d,
+                            start, rows, c0.kp, c0.vp, max_len=max(T))
+    else:
+        for i, c in enumerate(caches):
+            kt = k[i].transpose(0, 1)[:T[i]]     # [T, HK, D] view
+            vt = v[i].transpose(0, 1)[:T[i]]
+            cu = meta[2 * B + 2 * i:2 * B + 2 * i + 2]
+            if hasattr(c, "kp"):
+                row = (rows[i:i + 1].contiguous() if rows is not None else
+                       _to_device([list(c.table)], dev)
+                       if getattr(c, "table_dev_row", None) is None else
+                       c.table_dev_row.to(torch.int32)[None])
+                attn.kv_write_paged(kt, vt, row, start[i:i + 1], c.kp, c.vp,
+                                    cu_seqlens=cu, max_seqlen=T[i])
+            else:
+                W = c.k.shape[0]
+                per = W // PAGE
+                ring = torch.arange(per, dtype=torch.int32, device=dev)[None]
+                attn.kv_write_paged(kt, vt, ring, start[i:i + 1],
+                                    c.k.view(per, PAGE, *c.k.shape[1:]),
+                                    c.v.view(per, PAGE, *c.v.shape[1:]),
+                                    cu_seqlens=cu, max_seqlen=T[i],
+                                    table_wrap=per)
+    for i, c in enumerate(caches):
+        c.n = n0[i] + T[i]
+    return rows
 
 
 def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,

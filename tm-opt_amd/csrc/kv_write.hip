@@ -42,11 +42,16 @@ __global__ __launch_bounds__(256) void kv_write_slots_kernel(
 // rows (a mixed prefill + decode step) from dispatching tens of thousands of
 // empty work-groups; every load of a work-group (table entries, K and V) is
 // issued before its first store.
+//
+// Rows of a batch (`lens` given): sequence seq's tokens are rows
+// 0 .. lens[seq]-1 of its own source block, k + seq * k_sb (k_sb, v_sb in
+// 16-byte chunks), instead of rows cu_seqlens[seq] .. of one packed source.
 template <int R>
 __global__ __launch_bounds__(256) void kv_write_paged_kernel(
     const u32x4* __restrict__ k, const u32x4* __restrict__ v, int64_t k_st,
     int64_t k_sh, int64_t v_st, int64_t v_sh,
     const int32_t* __restrict__ cu_seqlens,
+    const int32_t* __restrict__ lens, int64_t k_sb, int64_t v_sb,
     const int32_t* __restrict__ start_pos,
     const int32_t* __restrict__ block_table, int64_t bt_stride,
     int table_wrap, int page_size, int HKV, int D16, u32x4* __restrict__ kp,
@@ -54,7 +59,12 @@ __global__ __launch_bounds__(256) void kv_write_paged_kernel(
   const int seq = blockIdx.y;
   const int per_tok = HKV * D16;
   int t0 = seq, len = 1;
-  if (cu_seqlens != nullptr) {
+  if (lens != nullptr) {
+    t0 = 0;
+    len = lens[seq];
+    k += seq * k_sb;
+    v += seq * v_sb;
+  } else if (cu_seqlens != nullptr) {
     t0 = cu_seqlens[seq];
     len = cu_seqlens[seq + 1] - t0;
   }
@@ -130,10 +140,13 @@ __device__ __forceinline__ uint32_t cm_slot(int d, int c) {
 }
 
 // grid (tiles, num_seqs, HKV), 256 threads
+// (rows of a batch: `lens` and the row strides k_sb / v_sb in elements,
+// as in kv_write_paged_kernel)
 __global__ __launch_bounds__(256) void kv_write_paged_cm_kernel(
     const __bf16* __restrict__ k, const __bf16* __restrict__ v, int64_t k_sh,
     int64_t k_sd, int64_t v_sh, int64_t v_sd,
     const int32_t* __restrict__ cu_seqlens,
+    const int32_t* __restrict__ lens, int64_t k_sb, int64_t v_sb,
     const int32_t* __restrict__ start_pos,
     const int32_t* __restrict__ block_table, int64_t bt_stride,
     int table_wrap, int page_size, int HKV, u32x4* __restrict__ kp,
@@ -142,7 +155,12 @@ __global__ __launch_bounds__(256) void kv_write_paged_cm_kernel(
   const int seq = blockIdx.y;
   const int h = blockIdx.z;
   int t0 = seq, len = 1;
-  if (cu_seqlens != nullptr) {
+  if (lens != nullptr) {
+    t0 = 0;
+    len = lens[seq];
+    k += seq * k_sb;
+    v += seq * v_sb;
+  } else if (cu_seqlens != nullptr) {
     t0 = cu_seqlens[seq];
     len = cu_seqlens[seq + 1] - t0;
   }
@@ -294,13 +312,16 @@ extern "C" int tmopt_kv_write_slots(const void* k, const void* v,
   return check_launch("kv_write_slots");
 }
 
-extern "C" int tmopt_kv_write_paged(
+// The paged write behind both entry points: runs of one packed source
+// (cu_seqlens; null: one token per sequence) or rows of a batch (lens and
+// the row strides k_sb / v_sb, in elements).
+static int write_paged(
     const void* k, const void* v, int64_t k_stride_tok, int64_t k_stride_head,
     int64_t k_stride_dim, int64_t v_stride_tok, int64_t v_stride_head,
-    int64_t v_stride_dim, const int32_t* cu_seqlens,
-    const int32_t* start_pos, int num_seqs, int max_seqlen,
-    const int32_t* block_table, int64_t bt_stride, int table_wrap,
-    int page_size, int HKV, int D, void* k_pool, void* v_pool,
+    int64_t v_stride_dim, const int32_t* cu_seqlens, const int32_t* lens,
+    int64_t k_sb, int64_t v_sb, const int32_t* start_pos, int num_seqs,
+    int max_seqlen, const int32_t* block_table, int64_t bt_stride,
+    int table_wrap, int page_size, int HKV, int D, void* k_pool, void* v_pool,
     int64_t num_pages, tmopt_stream_t stream) {
   clear_error();
   if (num_seqs == 0) return TMOPT_OK;
@@ -315,7 +336,12 @@ extern "C" int tmopt_kv_write_paged(
   TMOPT_REQUIRE(table_wrap == 0 || table_wrap <= bt_stride, TMOPT_EINVAL,
                 "kv_write_paged: table_wrap=%d exceeds bt_stride=%lld",
                 table_wrap, (long long)bt_stride);
-  if (cu_seqlens == nullptr) max_seqlen = 1;
+  TMOPT_REQUIRE(lens == nullptr || (k_sb >= 0 && v_sb >= 0 &&
+                                    k_sb % 8 == 0 && v_sb % 8 == 0),
+                TMOPT_EUNSUPPORTED,
+                "kv_write_paged: row strides must be multiples of 8 elements "
+                "(k %lld, v %lld)", (long long)k_sb, (long long)v_sb);
+  if (cu_seqlens == nullptr && lens == nullptr) max_seqlen = 1;
   TMOPT_REQUIRE(max_seqlen >= 0, TMOPT_EINVAL, "kv_write_paged: max_seqlen=%d",
                 max_seqlen);
   if (max_seqlen == 0) return TMOPT_OK;
@@ -351,8 +377,9 @@ extern "C" int tmopt_kv_write_paged(
                        dim3((unsigned)tiles, num_seqs, HKV), dim3(256), 0,
                        (hipStream_t)stream, (const __bf16*)k,
                        (const __bf16*)v, k_stride_head, k_stride_dim,
-                       v_stride_head, v_stride_dim, cu_seqlens, start_pos,
-                       block_table, bt_stride, table_wrap, page_size, HKV,
+                       v_stride_head, v_stride_dim, cu_seqlens, lens, k_sb,
+                       v_sb, start_pos, block_table, bt_stride, table_wrap,
+                       page_size, HKV,
                        (u32x4*)k_pool, (u32x4*)v_pool, num_pages);
     return check_launch("kv_write_paged (channel-major)");
   }
@@ -382,7 +409,8 @@ extern "C" int tmopt_kv_write_paged(
   hipLaunchKernelGGL(kv_write_paged_kernel<RR>, grid, dim3(256), 0, hs,       \
                      (const u32x4*)k, (const u32x4*)v, k_stride_tok / 8,     \
                      k_stride_head / 8, v_stride_tok / 8, v_stride_head / 8, \
-                     cu_seqlens, start_pos, block_table, bt_stride,          \
+                     cu_seqlens, lens, k_sb / 8, v_sb / 8, start_pos,        \
+                     block_table, bt_stride,                                 \
                      table_wrap, page_size, HKV, D16, (u32x4*)k_pool,        \
                      (u32x4*)v_pool, num_pages)
   switch (R) {
@@ -394,4 +422,37 @@ extern "C" int tmopt_kv_write_paged(
   }
 #undef TMOPT_KVW
   return check_launch("kv_write_paged");
+}
+
+extern "C" int tmopt_kv_write_paged(
+    const void* k, const void* v, int64_t k_stride_tok, int64_t k_stride_head,
+    int64_t k_stride_dim, int64_t v_stride_tok, int64_t v_stride_head,
+    int64_t v_stride_dim, const int32_t* cu_seqlens,
+    const int32_t* start_pos, int num_seqs, int max_seqlen,
+    const int32_t* block_table, int64_t bt_stride, int table_wrap,
+    int page_size, int HKV, int D, void* k_pool, void* v_pool,
+    int64_t num_pages, tmopt_stream_t stream) {
+  return write_paged(k, v, k_stride_tok, k_stride_head, k_stride_dim,
+                     v_stride_tok, v_stride_head, v_stride_dim, cu_seqlens,
+                     nullptr, 0, 0, start_pos, num_seqs, max_seqlen,
+                     block_table, bt_stride, table_wrap, page_size, HKV, D,
+                     k_pool, v_pool, num_pages, stream);
+}
+
+extern "C" int tmopt_kv_append_rows(
+    const void* k, const void* v, int64_t k_stride_row, int64_t k_stride_tok,
+    int64_t k_stride_head, int64_t k_stride_dim, int64_t v_stride_row,
+    int64_t v_stride_tok, int64_t v_stride_head, int64_t v_stride_dim,
+    const int32_t* lens, const int32_t* start_pos, int num_rows,
+    int max_len, const int32_t* block_table, int64_t bt_stride,
+    int table_wrap, int page_size, int HKV, int D, void* k_pool, void* v_pool,
+    int64_t num_pages, tmopt_stream_t stream) {
+  clear_error();
+  TMOPT_REQUIRE(num_rows <= 0 || lens != nullptr, TMOPT_EINVAL,
+                "kv_append_rows: lens is required");
+  return write_paged(k, v, k_stride_tok, k_stride_head, k_stride_dim,
+                     v_stride_tok, v_stride_head, v_stride_dim, nullptr, lens,
+                     k_stride_row, v_stride_row, start_pos, num_rows, max_len,
+                     block_table, bt_stride, table_wrap, page_size, HKV, D,
+                     k_pool, v_pool, num_pages, stream);
 }

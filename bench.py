@@ -14,14 +14,18 @@ launch stream (no event between launches: recording one there adds ~7 us
 to a ~100 us decode step).
 
 Secondary lines in "extra": config 3 (window-4096 decode), config 4 (varlen
-prefill, global and window 4096), the KV-cache write and config 5 (the
-66-layer mixed step as one hipGraph), each with its own roofline fraction;
+prefill, global and window 4096, and the same heads on 4 runs of 8192
+tokens), the KV-cache write and config 5 (the 66-layer mixed step as one
+hipGraph), each with its own roofline fraction;
 "adapters": the reference-signature entry points at the model's own layer
 shapes with the fused relative bias (attn_global, attn_swa,
 attn_prefill_fused beside the reference's published B300 times). The CPU
 baseline is the fp32 torch oracle on the host cores on the config-2 batch;
 "cpu_baselines" holds configs 3 and 4 and a scaled config-5 estimate, with
 the CPU model.
+
+In a full run the headline is timed last, after the other lines have
+brought the GPU to its working clocks.
 
 Prints ONE JSON line.
 """

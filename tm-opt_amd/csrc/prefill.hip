@@ -188,7 +188,9 @@ __device__ __forceinline__ int items_before(const PrefillArgs& a, int z,
 }
 
 struct Work {
-  int kvh, seq, qb;  // seq < 0: nothing to do
+  int kvh, seq, qb;    // seq < 0: nothing to do
+  int t0, len, prior;  // the run's first row, length and prior context
+  int total;           // cu[S]: rows of the launch (the LSE row length)
 };
 
 // Work item of this work-group (computed by every wave, identically).
@@ -212,8 +214,14 @@ __device__ __forceinline__ Work schedule(const PrefillArgs& a, int BQ,
     kvh = L % a.HKV;
     i = L / a.HKV;
   }
-  Work w{kvh, -1, 0};
-  const int nb0 = lane < a.S ? run_blocks(a, lane, BQ) : 0;
+  Work w{kvh, -1, 0, 0, 0, 0, 0};
+  // row start, end and prior context of the first 64 runs, one per lane:
+  // the item's own values are then lane reads, not a second round trip to
+  // memory after the search
+  const int c0 = lane < a.S ? a.cu[lane] : 0;
+  const int c1 = lane < a.S ? a.cu[lane + 1] : 0;
+  const int p0 = a.prior != nullptr && lane < a.S ? a.prior[lane] : 0;
+  const int nb0 = (c1 - c0 + BQ - 1) / BQ;
   const int total = items_before(a, a.nqb_max, BQ, lane, nb0);
   if (i >= total) return w;
   // level z: the last one with items_before(z) <= i
@@ -234,8 +242,20 @@ __device__ __forceinline__ Work schedule(const PrefillArgs& a, int BQ,
       const int rank = __builtin_amdgcn_mbcnt_hi(
           (uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
       const uint64_t hit = __builtin_amdgcn_ballot_w64(act && rank == rem);
-      w.seq = s0 + __builtin_ctzll(hit);
+      const int sl = __builtin_ctzll(hit);
+      w.seq = s0 + sl;
       w.qb = a.nqb_max - 1 - lo;
+      if (s0 == 0) {
+        w.t0 = __builtin_amdgcn_readlane(c0, sl);
+        w.len = __builtin_amdgcn_readlane(c1, sl) - w.t0;
+        w.prior = __builtin_amdgcn_readlane(p0, sl);
+      } else {
+        w.t0 = as_const(a.cu)[w.seq];
+        w.len = as_const(a.cu)[w.seq + 1] - w.t0;
+        w.prior = a.prior != nullptr ? as_const(a.prior)[w.seq] : 0;
+      }
+      w.total = a.S <= 64 ? __builtin_amdgcn_readlane(c1, a.S - 1)
+                          : as_const(a.cu)[a.S];
       return w;
     }
     rem -= pop;
@@ -270,10 +290,10 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   const int seq = wk.seq;
   const int qb = wk.qb;
 
-  const int t0 = as_const(a.cu)[seq];
-  const int len = as_const(a.cu)[seq + 1] - t0;
+  const int t0 = wk.t0;
+  const int len = wk.len;
   const int q0 = qb * BQ;
-  const int prior = a.prior ? as_const(a.prior)[seq] : 0;
+  const int prior = wk.prior;
   const int nk = prior + len;                 // keys of this run
   const int qn = min(BQ, len - q0);
   const int pos_lo = prior + q0;              // first query position
@@ -558,17 +578,20 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     }
   };
 
-  // per-element mask: causal, window, run end
+  // per-element mask: causal, window, run end. Element j of block kb holds
+  // key kt + 4 h2 + c with c = 32 kb + 8 (j >> 2) + (j & 3), a compile-time
+  // constant, and the keys a query sees form one interval lo < c <= hi per
+  // lane: two compares and a select per score.
   auto mask_tile = [&](f32x16 (&s)[2], int kt) {
+    const int base = kt + 4 * h2;
+    const int hi = qok ? min(qpos, nk - 1) - base : -1;
+    const int lo = a.window > 0 ? qpos - a.window - base : -1;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
-        const int kp = kt + 32 * kb + 8 * (j >> 2) + 4 * h2 + (j & 3);
-        const int dist = qpos - kp;
-        const bool ok = qok && dist >= 0 && kp < nk &&
-                        (a.window == 0 || dist < a.window);
-        s[kb][j] = ok ? s[kb][j] : -INFINITY;
+        const int c = 32 * kb + 8 * (j >> 2) + (j & 3);
+        s[kb][j] = (c <= hi && c > lo) ? s[kb][j] : -INFINITY;
       }
   };
 
@@ -633,9 +656,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // group 0 (its first softmax shares the slot of group 0's first
   // multiply), and both pass the same barriers in the same order.
   const int grp_id = w >> 2;
+  // A tile every valid query of the block sees whole. Query columns past
+  // the run end (a partial last block) are left unmasked there: their Q
+  // fragments are zero, so their scores are finite, and their rows are
+  // never stored (masking them sent every tile of such a block down the
+  // masked path, at about twice the cost per tile).
   auto full_tile = [&](int kt) {
     return (kt + kBN - 1 <= pos_lo) && (kt + kBN <= nk) &&
-           (a.window == 0 || pos_hi - kt < a.window) && (qn == BQ);
+           (a.window == 0 || pos_hi - kt < a.window);
   };
   f32x16 sc[2];        // scores of the tile after the one being multiplied
   bf16x8 pf[2][2];     // probabilities of the tile being multiplied
@@ -845,7 +873,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   const float inv = rejected ? __builtin_nanf("") :
                     l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
   if (a.lse && h2 == 0 && qok)
-    a.lse[(int64_t)head * as_const(a.cu)[a.S] + t0 + qi] =
+    a.lse[(int64_t)head * wk.total + t0 + qi] =
         rejected ? __builtin_nanf("") :
         l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : -INFINITY;
   // O^T goes through LDS (free after the last barrier) so that the global

@@ -5,8 +5,9 @@ Covers ragged lengths around the 32-query / 64-key tile edges, causal and
 windowed masks, GQA 4 and 8, strided inputs, chunked prefill reading prior
 context from a shuffled paged cache, the fused relative bias (band shorter
 than the runs, so most key tiles carry none; packed and paged sources), the
-q = 0 closed form (LSE = ln(#visible keys)), determinism, and config 4 at
-full size checked on sampled query rows.
+q = 0 closed form (LSE = ln(#visible keys)), determinism, config 4 at full
+size checked on sampled query rows, and the persistent grid's ticket
+counters (reuse of every counter slot, launches on two streams at once).
 """
 import math
 
@@ -518,3 +519,60 @@ def test_reject_flag_writes_nan(tm, dev):
     b = _gpu(tm, case, dev, reject=one)
     assert torch.equal(a[0], base[0]) and torch.equal(a[1], base[1])
     assert torch.isnan(b[0].float()).all() and torch.isnan(b[1]).all()
+
+
+def _dev_case(case, dev):
+    return (case.q.to(dev), case.k.to(dev), case.v.to(dev),
+            case.cu_seqlens.to(dev))
+
+
+def test_persistent_grid_counters_reset(tm, dev):
+    """Work-groups take their items from ticket counters in a per-launch
+    slot that the launch's last work-group clears: 300 launches in a row
+    (more than there are slots, so every slot is taken again) each write
+    every row (outputs pre-filled with NaN), bitwise equal to the first and
+    within tolerance of the oracle."""
+    case = _wl().make_prefill("pers", 25, lens=[1, 100, 37, 500, 64],
+                              window=0)
+    q, k, v, cu = _dev_case(case, dev)
+    T, HQ = case.q.shape[0], case.q.shape[1]
+    out0, lse0 = tm.prefill_varlen(q, k, v, cu, case.scale)
+    outs = [torch.empty_like(out0) for _ in range(3)]
+    lses = [torch.empty_like(lse0) for _ in range(3)]
+    for i in range(300):
+        o, l = outs[i % 3], lses[i % 3]
+        o.fill_(float("nan"))
+        l.fill_(float("nan"))
+        tm.prefill_varlen(q, k, v, cu, case.scale, out=o, lse=l)
+    torch.cuda.synchronize()
+    for o, l in zip(outs, lses):
+        assert torch.equal(o, out0) and torch.equal(l, lse0)
+    ref_o, ref_l = attn_ref.prefill_varlen(case.q, case.k, case.v,
+                                           case.cu_seqlens, case.scale)
+    assert_out_close(out0.cpu(), ref_o, "persistent")
+    assert_lse_close(lse0.cpu(), ref_l, "persistent")
+    assert out0.shape == (T, HQ, 128)
+
+
+def test_persistent_grid_two_streams(tm, dev):
+    """Launches in flight on two streams at once take different counter
+    slots: each stream's results equal its one-stream result."""
+    ca = _wl().make_prefill("pa", 26, lens=[700, 45, 1300], window=0)
+    cb = _wl().make_prefill("pb", 27, lens=[90, 2000], window=256, hq=64,
+                            hkv=8)
+    da, db = _dev_case(ca, dev), _dev_case(cb, dev)
+    ref_a = tm.prefill_varlen(*da, ca.scale)
+    ref_b = tm.prefill_varlen(*db, cb.scale, window=256)
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(dev), torch.cuda.Stream(dev)
+    res_a, res_b = [], []
+    for _ in range(10):
+        with torch.cuda.stream(sa):
+            res_a.append(tm.prefill_varlen(*da, ca.scale))
+        with torch.cuda.stream(sb):
+            res_b.append(tm.prefill_varlen(*db, cb.scale, window=256))
+    torch.cuda.synchronize()
+    for o, l in res_a:
+        assert torch.equal(o, ref_a[0]) and torch.equal(l, ref_a[1])
+    for o, l in res_b:
+        assert torch.equal(o, ref_b[0]) and torch.equal(l, ref_b[1])

@@ -358,22 +358,42 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   Runs rn{0, 0u};
   if (w == 0) rn = load_runs(a, BQ, lane, wk_lds + 32);
   int x = xcd_id();   // the XCD whose tickets wave 0 takes
-  int nsteal = 0;
   // (wave 0) a ticket on XCD x
   auto claim = [&]() {
     int t = 0;
     if (leader) t = atomicAdd(ctr + x, 1);
     return __builtin_amdgcn_readfirstlane(t);
   };
-  // (wave 0) the item of ticket j on XCD x; when x has none left, tickets
-  // of the next XCDs in turn (each counter only grows, so one miss each
-  // suffices)
+  // tickets of XCD xx that map to an item (schedule()'s XCD mapping
+  // inverted: valid tickets are j = 0 .. tickets_on(xx) - 1)
+  auto tickets_on = [&](int xx) {
+    if (a.HKV <= 8 && 8 % a.HKV == 0) {
+      const int R = 8 / a.HKV;
+      return max(0, (rn.items - xx % R + R - 1) / R);
+    }
+    if (a.HKV % 8 == 0) return rn.items * (a.HKV / 8);
+    return max(0, (rn.items * a.HKV - xx + 7) / 8);
+  };
+  // (wave 0) the item of ticket j on XCD x. When x has none left: one read
+  // of every XCD's counter, then a ticket on the nearest XCD that still has
+  // items. A claim that comes back empty (others took the last ones) means
+  // that XCD has run out as well, so each XCD fails at most once and nine
+  // rounds always end with an item or with every XCD done.
   auto find_work = [&](int j) {
     const int ln = opaque(lane);
     Work nw = schedule(a, BQ, ln, 8 * j + x, rn);
-    while (nw.seq < 0 && nsteal < 7) {
-      ++nsteal;
-      x = (x + 1) & 7;
+    for (int round = 0; nw.seq < 0 && round < 9; ++round) {
+      const int left =
+          ln < 8 ? tickets_on(ln) - __hip_atomic_load(ctr + ln,
+                                                      __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT)
+                 : 0;
+      const uint32_t m =
+          (uint32_t)__builtin_amdgcn_ballot_w64(left > 0) & 0xffu;
+      if (m == 0) break;
+      const int s0 = (x + 1) & 7;   // the nearest one after x, cyclically
+      const uint32_t rot = ((m >> s0) | (m << (8 - s0))) & 0xffu;
+      x = (s0 + __builtin_ctz(rot)) & 7;
       nw = schedule(a, BQ, ln, 8 * claim() + x, rn);
     }
     return nw;
@@ -997,9 +1017,15 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
       wait_vm<0>();
       read_q();
     }
-    // claim the ticket of the item after this one (used at the item's end)
+    // The ticket of the item after this one is claimed about three tiles
+    // before this item ends (by the leader, in group 0's tile loop): late
+    // enough that tickets go out in the order the work-groups finish, as a
+    // dispatcher would hand them out, which keeps the heaviest-first order
+    // when there are few items per CU; early enough that the atomic's
+    // latency is hidden.
     int nxt = 0;
-    if (leader) nxt = atomicAdd(ctr + x, 1);
+    const int claim_t = max(0, ntiles - 4);
+    if (leader && (rejected || ntiles == 1)) nxt = atomicAdd(ctr + x, 1);
     // ---- pipeline: 4 LDS stages, tiles issued three ahead -------------------
     // Slot 2t: group 0 multiplies tile t, group 1 does the softmax of tile t;
     // slot 2t+1: group 0 the softmax of tile t+1, group 1 multiplies tile t.
@@ -1054,6 +1080,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
       softmax_phase(sc, k_lo, true);
       bias_issue(k_lo + kBN);
       for (int t = 0; t + 1 < ntiles; ++t) {
+        if (leader && t == claim_t) nxt = atomicAdd(ctr + x, 1);
         if (t + 3 < ntiles) issue_tile(t + 3, (t + 3) & 3);
         mfma_phase(t, kWithS);
         __syncthreads();

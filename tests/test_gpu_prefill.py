@@ -6,8 +6,8 @@ windowed masks, GQA 4 and 8, strided inputs, chunked prefill reading prior
 context from a shuffled paged cache, the fused relative bias (band shorter
 than the runs, so most key tiles carry none; packed and paged sources), the
 q = 0 closed form (LSE = ln(#visible keys)), determinism, config 4 at full
-size checked on sampled query rows, and the persistent grid's ticket
-counters (reuse of every counter slot, launches on two streams at once).
+size checked on sampled query rows, and repeated launches back to back and
+on two streams at once.
 """
 import math
 
@@ -526,12 +526,11 @@ def _dev_case(case, dev):
             case.cu_seqlens.to(dev))
 
 
-def test_persistent_grid_counters_reset(tm, dev):
-    """Work-groups take their items from ticket counters in a per-launch
-    slot that the launch's last work-group clears: 300 launches in a row
-    (more than there are slots, so every slot is taken again) each write
-    every row (outputs pre-filled with NaN), bitwise equal to the first and
-    within tolerance of the oracle."""
+def test_repeated_launches_write_every_row(tm, dev):
+    """300 launches in a row, outputs pre-filled with NaN each time: every
+    launch writes every row and LSE entry, bitwise equal to the first, which
+    is within tolerance of the oracle (no state carries from one launch to
+    the next)."""
     case = _wl().make_prefill("pers", 25, lens=[1, 100, 37, 500, 64],
                               window=0)
     q, k, v, cu = _dev_case(case, dev)
@@ -554,9 +553,9 @@ def test_persistent_grid_counters_reset(tm, dev):
     assert out0.shape == (T, HQ, 128)
 
 
-def test_persistent_grid_two_streams(tm, dev):
-    """Launches in flight on two streams at once take different counter
-    slots: each stream's results equal its one-stream result."""
+def test_two_streams_at_once(tm, dev):
+    """Launches in flight on two streams at once (sharing the GPU's compute
+    units) give each stream's one-stream results, bitwise."""
     ca = _wl().make_prefill("pa", 26, lens=[700, 45, 1300], window=0)
     cb = _wl().make_prefill("pb", 27, lens=[90, 2000], window=256, hq=64,
                             hkv=8)

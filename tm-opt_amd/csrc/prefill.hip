@@ -34,21 +34,15 @@
 //  * Tiles wholly outside the causal/window band are never visited; only
 //    tiles that straddle the diagonal, the window start or the run end pay
 //    for per-element masking.
-//  * The (KV head, run, query block) items are ordered in "levels": level
-//    z holds query block nqb_max-1-z of every run that has one, so the
-//    heaviest blocks (most keys) go first and the light ones fill the tail.
-//    Empty (run, block) pairs are compacted away and the items are dealt to
-//    the 8 XCDs in turn, with each KV head kept on its own XCDs: every XCD
-//    gets an equal share of every level and only one KV head's keys pass
-//    through its L2. (A plain (head, run, block) grid maps runs to XCDs by
-//    index and left half of the XCDs idle for half the launch on mixed
-//    lengths.)
-//  * Persistent grid, one work-group per CU: each takes its XCD's items in
-//    that order from a ticket counter, and the next item's queries and first
-//    tiles load while the previous item's output is stored, so the
-//    work-group start and the first loads' latency are not paid per item.
-#include <atomic>
-#include <mutex>
+//  * A 1-D grid walks the (KV head, run, query block) items in "levels":
+//    level z holds query block nqb_max-1-z of every run that has one, so the
+//    heaviest blocks (most keys) are dispatched first and the light ones
+//    fill the tail. Empty (run, block) pairs are compacted away and the
+//    items are dealt to the 8 XCDs in turn (the dispatcher sends work-group
+//    i to XCD i % 8), with each KV head kept on its own XCDs: every XCD gets
+//    an equal share of every level and only one KV head's keys pass through
+//    its L2. A plain (head, run, block) grid maps runs to XCDs by index and
+//    left half of the XCDs idle for half the launch on mixed lengths.
 #include <type_traits>
 
 #include "common.h"
@@ -160,7 +154,6 @@ struct PrefillArgs {
   int64_t r_st, r_sh;
   int rel_extent;
   const int32_t* reject;  // optional device flag: nonzero = write NaN
-  int* sched;        // ticket counters of this launch (a slot of 16 ints)
 };
 
 // Sum over the wave, wave-uniform: within each 16-lane row by DPP (xor 1,
@@ -197,52 +190,17 @@ __device__ __forceinline__ int items_before(const PrefillArgs& a, int z,
 struct Work {
   int kvh, seq, qb;    // seq < 0: nothing to do
   int t0, len, prior;  // the run's first row, length and prior context
+  int total;           // cu[S]: rows of the launch (the LSE row length)
 };
 
-__device__ __forceinline__ void lds_st32(uint32_t addr, int v) {
-  *(__attribute__((address_space(3))) int*)(uintptr_t)addr = v;
-}
-__device__ __forceinline__ int lds_ld32(uint32_t addr) {
-  return *(const __attribute__((address_space(3))) int*)(uintptr_t)addr;
-}
-
-// The value unchanged, hidden from the optimiser: what is computed from it
-// stays where it is written instead of being hoisted out of a loop and
-// held in a register across the loop.
-__device__ __forceinline__ int opaque(int v) {
-  asm volatile("" : "+v"(v));
-  return v;
-}
-
-// Row start, end and prior context of the first 64 runs (one run per lane),
-// read from global memory once per work-group and kept in LDS; an item's
-// own values are then lane reads.
-struct Runs {
-  int items;      // items per KV head
-  uint32_t tab;   // LDS: c0[64], c1[64], p0[64] (cu[s], cu[s+1], prior[s])
-};
-
-// (the wave that loads the table is the one that reads it)
-__device__ __forceinline__ Runs load_runs(const PrefillArgs& a, int BQ,
-                                          int lane, uint32_t tab) {
-  const int c0 = lane < a.S ? a.cu[lane] : 0;
-  const int c1 = lane < a.S ? a.cu[lane + 1] : 0;
-  const int p0 = a.prior != nullptr && lane < a.S ? a.prior[lane] : 0;
-  lds_st32(tab + 4 * lane, c0);
-  lds_st32(tab + 256 + 4 * lane, c1);
-  lds_st32(tab + 512 + 4 * lane, p0);
-  return Runs{items_before(a, a.nqb_max, BQ, lane, (c1 - c0 + BQ - 1) / BQ),
-              tab};
-}
-
-// Work item L of the level order (computed by every wave, identically):
-// the one a grid with one work-group per item would give work-group L,
-// which runs on XCD L % 8 as the L/8-th one there. KV heads are spread
-// over the XCDs (8 % HKV == 0: 8/HKV XCDs per head; HKV % 8 == 0: HKV/8
-// heads per XCD; otherwise round robin), and each head's items, in level
-// order, are dealt to its XCDs in turn.
+// Work item of this work-group (computed by every wave, identically).
+// Work-group L runs on XCD L % 8 as the L/8-th one there. KV heads are
+// spread over the XCDs (8 % HKV == 0: 8/HKV XCDs per head; HKV % 8 == 0:
+// HKV/8 heads per XCD; otherwise round robin), and each head's items, in
+// level order, are dealt to its XCDs in turn.
 __device__ __forceinline__ Work schedule(const PrefillArgs& a, int BQ,
-                                         int lane, int L, const Runs& rn) {
+                                         int lane) {
+  const int L = blockIdx.x;
   int kvh, i;
   if (a.HKV <= 8 && 8 % a.HKV == 0) {
     const int R = 8 / a.HKV;
@@ -256,11 +214,16 @@ __device__ __forceinline__ Work schedule(const PrefillArgs& a, int BQ,
     kvh = L % a.HKV;
     i = L / a.HKV;
   }
-  Work w{kvh, -1, 0, 0, 0, 0};
-  if (kvh >= a.HKV || i >= rn.items) return w;
-  const int c0 = lds_ld32(rn.tab + 4 * lane);
-  const int c1 = lds_ld32(rn.tab + 256 + 4 * lane);
-  const int nb0 = (c1 - c0 + BQ - 1) / BQ;   // blocks of run `lane`
+  Work w{kvh, -1, 0, 0, 0, 0, 0};
+  // row start, end and prior context of the first 64 runs, one per lane:
+  // the item's own values are then lane reads, not a second round trip to
+  // memory after the search
+  const int c0 = lane < a.S ? a.cu[lane] : 0;
+  const int c1 = lane < a.S ? a.cu[lane + 1] : 0;
+  const int p0 = a.prior != nullptr && lane < a.S ? a.prior[lane] : 0;
+  const int nb0 = (c1 - c0 + BQ - 1) / BQ;
+  const int total = items_before(a, a.nqb_max, BQ, lane, nb0);
+  if (i >= total) return w;
   // level z: the last one with items_before(z) <= i
   int lo = 0, hi = a.nqb_max;
   while (hi - lo > 1) {
@@ -285,24 +248,19 @@ __device__ __forceinline__ Work schedule(const PrefillArgs& a, int BQ,
       if (s0 == 0) {
         w.t0 = __builtin_amdgcn_readlane(c0, sl);
         w.len = __builtin_amdgcn_readlane(c1, sl) - w.t0;
-        w.prior = lds_ld32(rn.tab + 512 + 4 * sl);
+        w.prior = __builtin_amdgcn_readlane(p0, sl);
       } else {
         w.t0 = as_const(a.cu)[w.seq];
         w.len = as_const(a.cu)[w.seq + 1] - w.t0;
         w.prior = a.prior != nullptr ? as_const(a.prior)[w.seq] : 0;
       }
+      w.total = a.S <= 64 ? __builtin_amdgcn_readlane(c1, a.S - 1)
+                          : as_const(a.cu)[a.S];
       return w;
     }
     rem -= pop;
   }
-  return w;  // not reached for i < items
-}
-
-// XCD of the calling wave (hardware register XCC_ID)
-__device__ __forceinline__ int xcd_id() {
-  unsigned v;
-  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
-  return (int)(v & 7u);
+  return w;  // not reached for i < total
 }
 
 // Where the keys of a run come from.
@@ -319,7 +277,6 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   constexpr bool OWN = SRC != kPaged;     // the run's keys from packed k/v
   constexpr int BQ = 256 / REP;   // queries per work-group
   constexpr int QSUB = BQ / 32;   // 32-query sub-blocks per head
-  constexpr bool VIS = REL;       // DMA the compiler can see (see dma())
   extern __shared__ __align__(16) char smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -327,816 +284,637 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int h2 = lane >> 5;       // lane half
+  const Work wk = schedule(a, BQ, lane);
+  if (wk.seq < 0) return;
+  const int kvh = wk.kvh;
+  const int seq = wk.seq;
+  const int qb = wk.qb;
+
+  const int t0 = wk.t0;
+  const int len = wk.len;
+  const int q0 = qb * BQ;
+  const int prior = wk.prior;
+  const int nk = prior + len;                 // keys of this run
+  const int qn = min(BQ, len - q0);
+  const int pos_lo = prior + q0;              // first query position
+  const int pos_hi = prior + q0 + qn - 1;     // last valid query position
+  // first key any query of the block may see; tiles start at a multiple of
+  // the tile width below it
+  const int kwin = a.window > 0 ? max(0, pos_lo - a.window + 1) : 0;
+  const int k_lo = (kwin / kBN) * kBN;
+  const int k_hi = pos_hi + 1;                // exclusive
+  const int ntiles = (k_hi - k_lo + kBN - 1) / kBN;
+
+  // ---- this wave's row block: head and 32-query sub-block ----------------
+  const int head = kvh * REP + w / QSUB;
+  const int qi = q0 + 32 * (w % QSUB) + l32;  // this lane's query (column)
+  const bool qok = qi < len;
+  const int qpos = prior + qi;
+
+  // ---- Q fragments: B operand of S^T (column = query, k = dims) --------
+  bf16x8 qf[8];   // loaded through LDS in the prologue below
+
+  // ---- tile loads: global -> LDS directly (buffer_load ... lds) ----------
+  // Wave w moves key rows 4w..4w+3 and 32+4w..32+4w+3 of the K and the V
+  // tile: one 1 KB instruction per 4 rows, lane l writing LDS bytes
+  // 16l..16l+15 of the 4-row block, i.e. row l>>4, physical 16-byte slot
+  // l&15. The lane fetches the logical chunk that belongs in that slot:
+  // K: slot c ^ (row & 15); V: 64-byte block b ^ (row & 3).
+  // Rows past the run end (and pages outside the pool) fall outside the
+  // buffer resource and arrive as zeros; tile offsets ride in the lane
+  // offset, which is what the hardware range-checks.
+  const int grp = lane >> 4, slot = lane & 15;
+  const int kchunk = slot ^ ((4 * w + grp) & 15);
+  const int vchunk = ((((slot >> 2) ^ grp) & 3) << 2) | (slot & 3);
   // LDS byte address of the dynamic shared block (0 here: the kernel has
   // no static LDS), a multiple of 256 as the fragment addressing assumes
   const uint32_t lds0 =
       (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)smem);
+  // packed rows of the run (keys 0.. of the run itself)
+  constexpr bool VIS = REL;   // DMA the compiler can see (see dma())
+  auto rk = mk_rsrc<VIS>(nullptr, 0u), rv = mk_rsrc<VIS>(nullptr, 0u);
+  int kst_b = 0, vst_b = 0, klane_p = 0, vlane_p = 0;
+  if constexpr (OWN) {
+    kst_b = (int)(a.k_st * 2);
+    vst_b = (int)(a.v_st * 2);
+    rk = mk_rsrc<VIS>(a.k + (int64_t)t0 * a.k_st + (int64_t)kvh * a.k_sh,
+                      (uint32_t)(((int64_t)(len - 1) * a.k_st + kD) * 2));
+    rv = mk_rsrc<VIS>(a.v + (int64_t)t0 * a.v_st + (int64_t)kvh * a.v_sh,
+                      (uint32_t)(((int64_t)(len - 1) * a.v_st + kD) * 2));
+    klane_p = grp * kst_b + 16 * kchunk;
+    vlane_p = grp * vst_b + 16 * vchunk;
+  }
+  // pool rows: keys below `plim` (all keys on the paged source, the prior
+  // context on the mixed one)
+  [[maybe_unused]] const int row_b = a.HKV * kD * 2;   // one token row
+  [[maybe_unused]] const int64_t page_b = (int64_t)kPage * row_b;
+  [[maybe_unused]] int klane = 0, vlane = 0;
+  if constexpr (POOL) {
+    klane = grp * row_b + kvh * (kD * 2) + 16 * kchunk;
+    vlane = grp * row_b + kvh * (kD * 2) + 16 * vchunk;
+  }
+  [[maybe_unused]] const int32_t __attribute__((address_space(4)))* trow =
+      POOL ? as_const(a.bt) + (int64_t)seq * a.bt_stride : nullptr;
+  [[maybe_unused]] const int plim = SRC == kMixed ? prior : nk;
 
-  // ---- work items ---------------------------------------------------------
-  // The grid is persistent: a work-group takes items one after another from
-  // the ticket counter of its XCD (ticket j there is item 8 j + x of the
-  // level order, the item a grid of one work-group per item would give
-  // work-group 8 j + x, which the dispatcher places on XCD x), and from the
-  // other XCDs' counters once its own has none left, so every item is
-  // taken whatever the placement. Wave 0 claims the tickets and looks the
-  // items up (alone: the lookup is mostly scalar code, and the CU's scalar
-  // unit is shared by its waves), and LDS hands each item to the others.
-  // The next ticket is claimed while the current item runs, and the next
-  // item's queries load while the current item's output is stored: a
-  // work-group start and the read of the run table are paid once per
-  // work-group, not once per item. The last work-group out clears the
-  // counters for the next launch on the same slot.
+  // Four pool rows key0..key0+3 (one page: key0 % 4 == 0) into LDS. The
+  // buffer resource covers only the page's rows in [kwin, plim): rows before
+  // the first key a query of the block may see and rows past the pool's
+  // part read as zeros and are never fetched (a ring page there holds an
+  // overwritten position, a windowed table may point it at a poison page),
+  // and so does a page whose table entry lies outside the pool or past the
+  // row's width. The lane offset is relative to the resource base, so the
+  // rows below it have negative offsets, i.e. out of range.
+  auto pool_dma = [&](int key0, uint32_t dk, uint32_t dv) {
+    if constexpr (POOL) {
+      const int lp = key0 >> 4;
+      const int col = a.table_wrap > 0 ? lp % a.table_wrap : lp;
+      const int pg = (unsigned)col < (unsigned)a.bt_width ? trow[col] : -1;
+      const int r_lo = min(kPage, max(0, kwin - kPage * lp));
+      const int r_hi = min(kPage, max(0, plim - kPage * lp));
+      const bool valid = (unsigned)pg < (unsigned)a.num_pages && r_hi > r_lo;
+      const uint32_t nrec = valid ? (uint32_t)((r_hi - r_lo) * row_b) : 0u;
+      const int64_t pofs = valid ? (int64_t)pg * page_b + r_lo * row_b : 0;
+      const int roff = ((key0 & (kPage - 1)) - r_lo) * row_b;
+      dma(mk_rsrc<VIS>(reinterpret_cast<const char*>(a.kpool) + pofs,
+                            nrec),
+               dk, klane + roff);
+      dma(mk_rsrc<VIS>(reinterpret_cast<const char*>(a.vpool) + pofs,
+                            nrec),
+               dv, vlane + roff);
+    }
+  };
+  // four packed rows j..j+3 of the run's own keys into LDS (rows past the
+  // run end are outside the resource: zeros)
+  auto own_dma = [&](int j, uint32_t dk, uint32_t dv) {
+    if constexpr (OWN) {
+      dma(rk, dk, klane_p + j * kst_b);
+      dma(rv, dv, vlane_p + j * vst_b);
+    }
+  };
+
+  // issue tile `t` (index from k_lo) into LDS stage `st`: 4 instructions
+  // per wave (2 with the source split inside a 4-row block: one per source,
+  // each under the exec mask of the lanes whose row it holds)
+  auto issue_tile = [&](int t, int st) {
+    const int kt = k_lo + t * kBN;
+    const uint32_t sb = lds0 + st * kStage;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r0 = 4 * w + 32 * i;          // first row of the block
+      const uint32_t dk = sb + r0 * kRowB, dv = dk + kTileB;
+      const int key0 = kt + r0;
+      if constexpr (SRC == kPacked) {
+        own_dma(key0, dk, dv);
+      } else if constexpr (SRC == kPaged) {
+        pool_dma(key0, dk, dv);
+      } else {
+        if (key0 + 4 <= plim) {
+          pool_dma(key0, dk, dv);
+        } else if (key0 >= plim) {
+          own_dma(key0 - plim, dk, dv);
+        } else {
+          // lane group grp holds row key0 + grp
+          if (key0 + grp < plim) pool_dma(key0, dk, dv);
+          else own_dma(key0 - plim, dk, dv);
+        }
+      }
+    }
+  };
+
+  // ---- LDS fragment addresses -------------------------------------------
+  // K fragment (kb, kk) of lane (l32, h2): row 32 kb + l32, logical chunk
+  // 2 kk + h2 -> slot (2 kk + h2) ^ (l32 & 15) = (h2 ^ (l32 & 15)) ^ 2 kk.
+  const uint32_t ka0 = (uint32_t)(l32 * kRowB + 16 * (h2 ^ (l32 & 15)));
+  // V^T fragment (db, kb, kk) by two transposed reads: within each 16-lane
+  // group, source lane s names key kbase + (s >> 2), dims 4 (s & 3)..+3 of
+  // a 16-dim half; lane i of the group then holds dim dbase + i of keys
+  // kbase..kbase+3. kbase = 32 kb + 16 kk + 4 h2 (+8 for the second read),
+  // dbase = 32 db + 16 (l32 >> 4), which matches the order of this lane's
+  // probabilities (keys 16 kk + 4 h2 + 0..3 and 16 kk + 8 + 4 h2 + 0..3).
+  const int s16 = lane & 15;
+  const uint32_t va0 = (uint32_t)((4 * h2 + (s16 >> 2)) * kRowB +
+                                  64 * (s16 >> 2) + 32 * ((lane >> 4) & 1) +
+                                  8 * (s16 & 3));
+
+  // S^T = K.Q^T for the tile in `stage` (keys on M, queries on N)
+  auto scores = [&](int stage, f32x16 (&s)[2]) {
+    const uint32_t kb0 = ka0 + lds0 + stage * kStage;
+    s[0] = f32x16{};
+    s[1] = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const bf16x8 kf = lds_ld128((kb0 ^ (32u * kk)) + 32 * kb * kRowB);
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kb], 0,
+                                                        0, 0);
+      }
+  };
+
+  // V^T fragment (db, kb, kk) of the tile whose V rows start at vbase
+  auto vfrag = [&](uint32_t vdb, int kb, int kk) {
+    const uint32_t p = vdb + (32 * kb + 16 * kk) * kRowB;
+    const bf16x4 lo = lds_tr16(p);
+    const bf16x4 hi = lds_tr16(p + 8 * kRowB);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+
+  // Fused bias rows of this wave's 32 queries: one buffer resource from
+  // the first query's row (lane offsets: row l32, 32-bit), covering the
+  // rows of the run only, so reads past them return zeros.
+  // (The resource starts at the dword holding that row's first value and
+  // ends at the dword holding the last row's last value, so that the dword
+  // loads below are aligned whatever the strides and every dword holding a
+  // value of the rows is in range.)
+  const int rel_row0 = q0 + 32 * (w % QSUB);
+  const int rel_nrow = REL ? min(32, len - rel_row0) : 0;
+  const char* const rel_first =
+      REL ? reinterpret_cast<const char*>(a.rel + (int64_t)(t0 + rel_row0) *
+                                                      a.r_st +
+                                          (int64_t)head * a.r_sh)
+          : nullptr;
+  const int rel_mis = (int)((uintptr_t)rel_first & 3);   // 0 or 2
+  [[maybe_unused]] const __amdgpu_buffer_rsrc_t rrel =
+      __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<char*>(rel_first - rel_mis), (short)0,
+          rel_nrow > 0 ? ((int)(((int64_t)(rel_nrow - 1) * a.r_st +
+                                 a.rel_extent) * 2) + rel_mis + 3) & ~3
+                       : 0,
+          0x00020000);
+  [[maybe_unused]] const int rrow_b =
+      REL ? rel_mis + l32 * (int)(a.r_st * 2) : 0;
+
+  // The fused bias of a key tile, loaded one softmax ahead (bias_issue)
+  // and applied in the softmax (bias_apply). The lane's keys come in runs
+  // of four (key0 .. key0+3, dist d0 .. d0-3), whose four bf16 values are
+  // adjacent in the row: the three dwords from the one holding rel[d0-3],
+  // realigned by 0 or 2 bytes. The range check is per dword and the
+  // resource ends at a dword boundary, so every value of the rows arrives;
+  // the whole offset goes in the lane register, where the check sees it.
+  // Every call issues exactly 8 loads (a tile outside the band or past the
+  // run reads nothing), so the wave's load counts stay fixed: the waits
+  // for them never reach the tile DMA issued after them.
+  typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+  [[maybe_unused]] u32x3 rb[8];
+  [[maybe_unused]] auto bias_issue = [&](int kt) {
+    if constexpr (REL) {
+      const bool band_tile = kt < k_hi && pos_lo - (kt + kBN - 1) < a.rel_extent;
+      // byte offset of rel[d0 - 3] for kb = g = 0, opaque to the compiler
+      // so that the eight offsets are derived from it here rather than
+      // hoisted out of the key loop as eight live registers
+      int base = rrow_b + 2 * (qpos - kt - 4 * h2 - 3);
+      asm volatile("" : "+v"(base));
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int b4 = (base - 64 * kb - 16 * g) & ~3;
+          // before the first row (row 0 near dist 0): from the row start,
+          // shifted back into place by bias_apply
+          int off = band_tile ? (b4 < 0 ? 0 : b4) : 0x7ffffff0;
+          asm volatile("" : "+v"(off));
+          rb[4 * kb + g] = __builtin_bit_cast(
+              u32x3, __builtin_amdgcn_raw_buffer_load_b96(rrel, off, 0, 0));
+        }
+    }
+  };
+  // the scores move to the log2 domain: s*scale*log2e + rel*log2e,
+  // rel[q, h, dist] for 0 <= dist < E, zero outside
+  // Byte shift that realigns a lane's runs: the same on every tile (tile
+  // starts are multiples of 64 keys, so only the row's parity matters).
+  [[maybe_unused]] const uint32_t rel_sh =
+      REL ? (uint32_t)((rrow_b + 2 * (qpos - 3)) & 3) : 0u;
+  // The scores of a bias tile move to the natural-log domain with the bias
+  // added: s*scale + rel[q, h, dist] for 0 <= dist < E, zero outside.
+  // FAST (a whole tile with every dist in [0, E) for every query: no mask,
+  // no band test, every run starts inside its row) costs two byte-aligns
+  // per run and two instructions per score; the checked path handles the
+  // tiles at the diagonal, the run ends and the band edge.
+  [[maybe_unused]] auto bias_apply = [&](f32x16 (&s)[2], int kt, auto fast_c) {
+    constexpr bool fast = decltype(fast_c)::value;
+    if constexpr (REL) {
+      // dist of the lane's first key for kb = g = 0 (opaque, as above)
+      int dq = qpos - kt - 4 * h2;
+      asm volatile("" : "+v"(dq));
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = dq - 32 * kb - 8 * g;
+          const uint32_t x0 = rb[4 * kb + g][0], x1 = rb[4 * kb + g][1],
+                         x2 = rb[4 * kb + g][2];
+          uint32_t w0, w1;
+          if constexpr (fast) {
+            w0 = __builtin_amdgcn_alignbyte(x1, x0, rel_sh);
+            w1 = __builtin_amdgcn_alignbyte(x2, x1, rel_sh);
+          } else {
+            const int b = rrow_b + 2 * (d0 - 3);
+            const int b4 = b & ~3;
+            // dwords the load started after the one holding rel[d0-3]
+            // (only when that one lies before the row; 3 or more: every
+            // dist of the run is negative, i.e. masked)
+            const int kd = b4 < 0 ? (-b4) >> 2 : 0;
+            const uint32_t y0 = kd == 0 ? x0 : 0u;
+            const uint32_t y1 = kd == 0 ? x1 : (kd == 1 ? x0 : 0u);
+            const uint32_t y2 = kd == 0 ? x2 : (kd == 1 ? x1 : x0);
+            w0 = __builtin_amdgcn_alignbyte(y1, y0, rel_sh);
+            w1 = __builtin_amdgcn_alignbyte(y2, y1, rel_sh);
+          }
+          // element 4g + i is key0 + i, dist d0 - i
+          const uint32_t hv[4] = {w1 & 0xffff0000u, w1 << 16,
+                                  w0 & 0xffff0000u, w0 << 16};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float bias = __builtin_bit_cast(float, hv[i]);
+            if constexpr (!fast) {
+              const int dist = d0 - i;
+              const bool band = qok && dist >= 0 && dist < a.rel_extent;
+              bias = band ? bias : 0.0f;
+            }
+            s[kb][4 * g + i] = __builtin_fmaf(s[kb][4 * g + i], a.scale, bias);
+          }
+        }
+    }
+  };
+
+  // per-element mask: causal, window, run end. Element j of block kb holds
+  // key kt + 4 h2 + c with c = 32 kb + 8 (j >> 2) + (j & 3), a compile-time
+  // constant, and the keys a query sees form one interval lo < c <= hi per
+  // lane: two compares and a select per score.
+  auto mask_tile = [&](f32x16 (&s)[2], int kt) {
+    const int base = kt + 4 * h2;
+    const int hi = qok ? min(qpos, nk - 1) - base : -1;
+    const int lo = a.window > 0 ? qpos - a.window - base : -1;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int c = 32 * kb + 8 * (j >> 2) + (j & 3);
+        s[kb][j] = (c <= hi && c > lo) ? s[kb][j] : -INFINITY;
+      }
+  };
+
+  // ---- accumulators -----------------------------------------------------
+  f32x16 o_acc[4];
+#pragma unroll
+  for (int db = 0; db < 4; ++db) o_acc[db] = f32x16{};
+  float m_run = -INFINITY;
+  float l_part = 0.0f;
+  // Without a bias the max runs on the raw scores (scale > 0 commutes with
+  // max) and each probability is one fma + exp2: p = 2^(s*scale*log2e - m).
+  // (on tiles that carry the fused bias the scores are s*scale + bias,
+  // and the factor is log2e)
+
+  // Lazy rescaling: the running max (log2 domain) only moves when the
+  // tile's max exceeds it by more than kLazy, so probabilities stay below
+  // 2^kLazy and O^T / l are rescaled on few tiles; O / l and the LSE are
+  // exact for any reference point.
+  auto new_max = [&](float mx, float sl2, bool& move, float& m_use) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(
+        __builtin_bit_cast(uint32_t, mx), __builtin_bit_cast(uint32_t, mx),
+        false, false);
+    mx = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]),
+               __builtin_bit_cast(float, (uint32_t)sw[1]));
+    const float m_cand = mx * sl2;
+    move = m_cand > m_run + kLazy;
+    const float m_new = move ? m_cand : m_run;
+    m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = move ? fast_exp2(m_run - m_use) : 1.0f;
+    m_run = m_new;
+    return alpha;
+  };
+  // probability pair q (kb = q >> 3, kk = (q >> 2) & 1, e = q & 3)
+  auto prob_pair = [&](const f32x16 (&s)[2], int q, float sl2, float m_use,
+                       float& psum) {
+    const int kb = q >> 3, kk = (q >> 2) & 1, e = q & 3;
+    const float p0 =
+        fast_exp2(__builtin_fmaf(s[kb][8 * kk + 2 * e], sl2, -m_use));
+    const float p1 =
+        fast_exp2(__builtin_fmaf(s[kb][8 * kk + 2 * e + 1], sl2, -m_use));
+    psum += p0 + p1;
+    return pack_bf16x2_rn(p0, p1);
+  };
+  auto pack_p = [&](const uint32_t (&pw)[16], bf16x8 (&pf)[2][2]) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int q = 8 * kb + 4 * kk;
+        pf[kb][kk] = __builtin_bit_cast(
+            bf16x8, u32x4{pw[q], pw[q + 1], pw[q + 2], pw[q + 3]});
+      }
+  };
+
+  // ---- two wave groups in ping-pong ---------------------------------------
+  // Waves 0-3 and 4-7 (one of each per SIMD) alternate between an MFMA
+  // phase (P.V of tile t and the scores of tile t+1: 32 MFMAs, fragment
+  // reads, hardly any VALU) and a softmax phase (the online softmax of those
+  // scores: VALU only), half a tile apart: while one wave of a SIMD keeps
+  // the matrix core busy the other one uses the vector ALU. A work-group
+  // barrier ends every phase (two per tile); group 1 runs one phase behind
+  // group 0 (its first softmax shares the slot of group 0's first
+  // multiply), and both pass the same barriers in the same order.
+  const int grp_id = w >> 2;
+  // A tile every valid query of the block sees whole. Query columns past
+  // the run end (a partial last block) are left unmasked there: their Q
+  // fragments are zero, so their scores are finite, and their rows are
+  // never stored (masking them sent every tile of such a block down the
+  // masked path, at about twice the cost per tile).
+  auto full_tile = [&](int kt) {
+    return (kt + kBN - 1 <= pos_lo) && (kt + kBN <= nk) &&
+           (a.window == 0 || pos_hi - kt < a.window);
+  };
+  f32x16 sc[2];        // scores of the tile after the one being multiplied
+  bf16x8 pf[2][2];     // probabilities of the tile being multiplied
+
+  // softmax of scores `s` of the tile at kt (masking when needed): P^T
+  // fragments, running max / sum update, O^T rescale when the max moved
+  auto softmax_phase = [&](f32x16 (&s)[2], int kt, bool first) {
+    // the bias band: some pair of the tile has dist = q - k < E (the
+    // smallest dist is pos_lo - (kt + 63))
+    const bool with_bias = REL && pos_lo - (kt + kBN - 1) < a.rel_extent;
+    const bool full = full_tile(kt);
+    if constexpr (REL) {
+      if (with_bias) {
+        if (full && pos_hi - kt < a.rel_extent)
+          bias_apply(s, kt, std::true_type{});
+        else
+          bias_apply(s, kt, std::false_type{});
+      }
+    }
+    if (!full) mask_tile(s, kt);
+    const float sl2 = with_bias ? kLog2e : a.scale_log2;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 16; j += 2)
+        mx = fmaxf(fmaxf(mx, s[kb][j]), s[kb][j + 1]);
+    bool move;
+    float m_use;
+    const float alpha = new_max(mx, sl2, move, m_use);
+    float psum = 0.0f;
+    uint32_t pw[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) pw[q] = prob_pair(s, q, sl2, m_use, psum);
+    pack_p(pw, pf);
+    l_part = l_part * alpha + psum;
+    // O^T holds the tiles before this one: rescale it to the new reference
+    // (in place, each product tied to its accumulator register: a plain
+    // multiply under the branch leaves the compiler a merge of two copies
+    // of O^T, which it resolves with 32 register-pair moves on every tile)
+    if (!first && __builtin_amdgcn_ballot_w64(move)) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          float x = o_acc[db][j];
+          asm volatile("v_mul_f32 %0, %1, %0" : "+v"(x) : "v"(alpha));
+          o_acc[db][j] = x;
+        }
+    }
+  };
+
+  // MFMA phase of tile t: O^T += V^T.P^T for tile t (four accumulators in
+  // turn) interleaved with the scores of tile t+1 (two accumulators), the
+  // V^T and K fragments read kRing - 1 MFMAs ahead (3: measured ~1% over 4
+  // and 5 ahead on 4K-16K runs)
+  auto mfma_phase = [&](int t, auto with_s_c) {
+    // (with_s as a type: one straight-line copy per case, no branch between
+    // the MFMAs)
+    constexpr bool with_s = decltype(with_s_c)::value;
+    // the SIMD's issue port goes to this wave's MFMAs first; the softmax
+    // wave fills the slots in between (measured ~2% over equal priority)
+    __builtin_amdgcn_s_setprio(1);
+    const uint32_t vb = va0 + lds0 + (t & 3) * kStage + kTileB;
+    const uint32_t kb0 = ka0 + lds0 + ((t + 1) & 3) * kStage;
+    auto vf_n = [&](int n) {
+      const int db = n & 3, kb = n >> 3, kk = (n >> 2) & 1;
+      return vfrag(vb ^ (64u * db), kb, kk);
+    };
+    auto kf_n = [&](int n) {
+      return lds_ld128((kb0 ^ (32u * (n >> 1))) + 32 * (n & 1) * kRowB);
+    };
+    constexpr int R = kRing;     // fragments read R - 1 MFMAs ahead
+    bf16x8 vf[R], kf[R];
+#pragma unroll
+    for (int i = 0; i < R - 1; ++i) {
+      vf[i] = vf_n(i);
+      if (with_s) kf[i] = kf_n(i);
+    }
+#pragma unroll
+    for (int n = 0; n < 16; ++n) {
+      if (n + R - 1 < 16) vf[(n + R - 1) % R] = vf_n(n + R - 1);
+      if (with_s && n + R - 1 < 16) kf[(n + R - 1) % R] = kf_n(n + R - 1);
+      const int db = n & 3, kb = n >> 3, kk = (n >> 2) & 1;
+      o_acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          vf[n % R], pf[kb][kk], o_acc[db], 0, 0, 0);
+      if (with_s) {
+        const int skb = n & 1, skk = n >> 1;
+        sc[skb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+            kf[n % R], qf[skk], n < 2 ? f32x16{} : sc[skb], 0, 0, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_setprio(0);
+  };
+
   // A caller that found its inputs invalid on the device (without a host
   // sync) sets *reject: every output row and LSE entry of the launch is then
   // NaN and no key is read.
   const bool rejected = a.reject != nullptr && as_const(a.reject)[0] != 0;
-  int* const ctr = a.sched;         // [0, 8): tickets per XCD, [8]: done
-  const bool leader = tid == 0;
-  // past the four stages: the item being handed over (8 ints), then the
-  // run table (read by wave 0 only)
-  const uint32_t wk_lds = lds0 + kNStage * kStage;
-  Runs rn{0, 0u};
-  if (w == 0) rn = load_runs(a, BQ, lane, wk_lds + 32);
-  int x = xcd_id();   // the XCD whose tickets wave 0 takes
-  // (wave 0) a ticket on XCD x
-  auto claim = [&]() {
-    int t = 0;
-    if (leader) t = atomicAdd(ctr + x, 1);
-    return __builtin_amdgcn_readfirstlane(t);
-  };
-  // tickets of XCD xx that map to an item (schedule()'s XCD mapping
-  // inverted: valid tickets are j = 0 .. tickets_on(xx) - 1)
-  auto tickets_on = [&](int xx) {
-    if (a.HKV <= 8 && 8 % a.HKV == 0) {
-      const int R = 8 / a.HKV;
-      return max(0, (rn.items - xx % R + R - 1) / R);
-    }
-    if (a.HKV % 8 == 0) return rn.items * (a.HKV / 8);
-    return max(0, (rn.items * a.HKV - xx + 7) / 8);
-  };
-  // (wave 0) the item of ticket j on XCD x. When x has none left: one read
-  // of every XCD's counter, then a ticket on the nearest XCD that still has
-  // items. A claim that comes back empty (others took the last ones) means
-  // that XCD has run out as well, so each XCD fails at most once and nine
-  // rounds always end with an item or with every XCD done.
-  auto find_work = [&](int j) {
-    const int ln = opaque(lane);
-    Work nw = schedule(a, BQ, ln, 8 * j + x, rn);
-    for (int round = 0; nw.seq < 0 && round < 9; ++round) {
-      const int left =
-          ln < 8 ? tickets_on(ln) - __hip_atomic_load(ctr + ln,
-                                                      __ATOMIC_RELAXED,
-                                                      __HIP_MEMORY_SCOPE_AGENT)
-                 : 0;
-      const uint32_t m =
-          (uint32_t)__builtin_amdgcn_ballot_w64(left > 0) & 0xffu;
-      if (m == 0) break;
-      const int s0 = (x + 1) & 7;   // the nearest one after x, cyclically
-      const uint32_t rot = ((m >> s0) | (m << (8 - s0))) & 0xffu;
-      x = (s0 + __builtin_ctz(rot)) & 7;
-      nw = schedule(a, BQ, ln, 8 * claim() + x, rn);
-    }
-    return nw;
-  };
-  // wave 0's item to every wave; the barrier also tells wave 0 that every
-  // wave has read the previous one (read right after the previous barrier)
-  auto hand_over = [&](Work nw) {
-    if (leader) {
-      lds_st32(wk_lds, nw.kvh);
-      lds_st32(wk_lds + 4, nw.seq);
-      lds_st32(wk_lds + 8, nw.qb);
-      lds_st32(wk_lds + 12, nw.t0);
-      lds_st32(wk_lds + 16, nw.len);
-      lds_st32(wk_lds + 20, nw.prior);
-    }
-    __syncthreads();
-    auto rd = [&](int o) {
-      return __builtin_amdgcn_readfirstlane(lds_ld32(wk_lds + o));
-    };
-    return Work{rd(0), rd(4), rd(8), rd(12), rd(16), rd(20)};
-  };
-  // rows of the launch (cu[S]), the LSE row length
-  const int lse_rows = a.lse ? as_const(a.cu)[a.S] : 0;
-
-  // ---- accumulators and query fragments ----------------------------------
-  f32x16 o_acc[4];     // O^T of the item (32 dims x 32 queries per block)
-  float m_run = -INFINITY;
-  float l_part = 0.0f;
-  // Q fragments of the item (B operand of S^T: column = query, k = dims).
-  // The rows come by the same direct loads as the tiles, into this wave's
-  // 8 KB of LDS stages 2 and 3 (1 KB = 4 rows per instruction, 16-byte
-  // chunks swizzled by row & 15; rows past the run end arrive as zeros),
-  // issued at the end of the previous item, when every stage is free; the
-  // wave reads its fragments back at the start of the item, before its
-  // output staging reuses the same bytes.
-  bf16x8 qf[8];
-  auto load_q = [&](const Work& it) {
-    const int ln = opaque(lane), grp = ln >> 4, slot = ln & 15;
-    const uint32_t qlds = lds0 + 2 * kStage + (uint32_t)w * (32 * kRowB);
-    const int qrow0 = it.qb * BQ + 32 * (w % QSUB);
-    const int head = it.kvh * REP + w / QSUB;
-    const int64_t qspan = ((int64_t)(it.len - qrow0 - 1) * a.q_st + kD) * 2;
+  if (!rejected) {
+  // ---- pipeline: 4 LDS stages, tiles issued three ahead -------------------
+  // Slot 2t: group 0 multiplies tile t, group 1 does the softmax of tile t;
+  // slot 2t+1: group 0 the softmax of tile t+1, group 1 multiplies tile t.
+  // Tile t+3 goes out at the start of slot 2t into the stage of tile t-1
+  // (last read in slot 2t-1) and must be in LDS before slot 2t+4; each
+  // wave waits for its own part at the end of every odd slot, before the
+  // barrier that publishes it (4 instructions per wave per tile).
+  // The queries come first, by the same direct loads: the wave's 32 rows
+  // (1 KB = 4 rows per instruction, 16-byte chunks swizzled by row & 15)
+  // into stages 2 and 3, which hold no tile until tile 2 goes out after
+  // every wave has its fragments; rows past the run end arrive as zeros.
+  const uint32_t qlds = lds0 + 2 * kStage + (uint32_t)w * (32 * kRowB);
+  {
+    const int qrow0 = q0 + 32 * (w % QSUB);
+    const int64_t qspan = ((int64_t)(len - qrow0 - 1) * a.q_st + kD) * 2;
     const auto rq = mk_rsrc<VIS>(
-        a.q + (int64_t)(it.t0 + qrow0) * a.q_st + (int64_t)head * a.q_sh,
-        qrow0 < it.len ? (uint32_t)qspan : 0u);
+        a.q + (int64_t)(t0 + qrow0) * a.q_st + (int64_t)head * a.q_sh,
+        qrow0 < len ? (uint32_t)qspan : 0u);
     const int qst_b = (int)(a.q_st * 2);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int r = 4 * i + grp;
       dma(rq, qlds + i * 1024, r * qst_b + 16 * (slot ^ (r & 15)));
     }
-  };
-  auto read_q = [&]() {
-    const int ln = opaque(lane), l32 = ln & 31, h2 = ln >> 5;
-    const uint32_t qlds = lds0 + 2 * kStage + (uint32_t)w * (32 * kRowB);
+  }
+  issue_tile(0, 0);
+  if (ntiles > 1) issue_tile(1, 1);
+  wait_vm<0>();
+  __syncthreads();
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-      qf[kk] = lds_ld128(qlds + l32 * kRowB +
-                         16 * ((2 * kk + h2) ^ (l32 & 15)));
-  };
-  struct Fin {         // where an item's output goes
-    int head, t0, len, qrow0;
-  };
-  Fin prev{0, 0, 0, 0};
-  float prev_lse = 0.0f;
-  bool have_prev = false;
-  // The output of an item leaves in two steps: stage_output (at the item's
-  // end) normalises O^T into LDS stages 2 and 3, and flush_output (at the
-  // next item's start, after that item's first tile loads went out) copies
-  // the rows to global memory. The stores are issued after those loads, so
-  // the wait for the loads before the barrier does not wait for the stores.
-  // Stage 2 is free for the next tile only after that barrier. O^T goes
-  // through LDS so that the global stores are whole rows: the wave writes
-  // its 32 x 128 block query-major (256-byte rows, 16-byte chunks swizzled
-  // by row & 15, so neither the 8-byte writes nor the 16-byte reads
-  // conflict), then each store instruction covers 4 complete rows (16 lanes
-  // x 16 bytes per row) instead of 16 bytes of 32 rows.
-  // (lane values re-derived from an opaque lane index here, in load_q and
-  // at the top of every item: otherwise the compiler hoists what derives
-  // from the lane out of the item loop and holds it in registers through
-  // the tile loops, and spills)
-  auto stage_output = [&]() {
-    const int ln = opaque(lane), l32 = ln & 31, h2 = ln >> 5;
-    const float l_tot = l_part + __shfl_xor(l_part, 32);
-    const float inv = rejected ? __builtin_nanf("") :
-                      l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    const uint32_t ob = lds0 + 2 * kStage + (uint32_t)w * (32 * kRowB);
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int g4 = 0; g4 < 4; ++g4) {
-        const f32x16& o = o_acc[db];
-        const uint32_t w0 = pack_bf16x2(f32_to_bf16_bits(o[4 * g4] * inv),
-                                        f32_to_bf16_bits(o[4 * g4 + 1] * inv));
-        const uint32_t w1 = pack_bf16x2(f32_to_bf16_bits(o[4 * g4 + 2] * inv),
-                                        f32_to_bf16_bits(o[4 * g4 + 3] * inv));
-        const int c = 4 * db + g4;    // 16-byte chunk: dims 8c .. 8c+7
-        lds_st64(ob + l32 * kRowB + 16 * (c ^ (l32 & 15)) + 8 * h2,
-                 u32x2{w0, w1});
-      }
-    wave_lds_sync();
-    // the LSE of the lane's query (natural log)
-    return rejected ? __builtin_nanf("") :
-           l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : -INFINITY;
-  };
-  // Every store is issued (rows past the run end fall outside the buffer
-  // resource and are dropped), so the count is fixed: 8 row stores (16 when
-  // the rows are not 16-byte aligned) and one LSE store. Returns it.
-  const bool al16 = ((a.o_st | a.o_sh) & 7) == 0 &&
-                    ((uintptr_t)a.out & 15) == 0;
-  auto flush_output = [&](const Fin& f, float lse_v) {
-    const int ln = opaque(lane), l32 = ln & 31, h2 = ln >> 5;
-    const uint32_t ob = lds0 + 2 * kStage + (uint32_t)w * (32 * kRowB);
-    const int nrow = max(0, min(32, f.len - f.qrow0));
-    const auto ro = __builtin_amdgcn_make_buffer_rsrc(
-        a.out + (int64_t)(f.t0 + f.qrow0) * a.o_st + (int64_t)f.head * a.o_sh,
-        (short)0, nrow > 0 ? (int)(((int64_t)(nrow - 1) * a.o_st + kD) * 2) : 0,
-        0x00020000);
-    const int c16 = ln & 15;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = 4 * i + (ln >> 4);
-      const u32x4 v16 = __builtin_bit_cast(
-          u32x4, lds_ld128(ob + r * kRowB + 16 * (c16 ^ (r & 15))));
-      const int off = r * (int)(a.o_st * 2) + 16 * c16;
-      if (al16) {
-        __builtin_amdgcn_raw_buffer_store_b128(v16, ro, off, 0, 0);
-      } else {
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{v16[0], v16[1]}, ro, off,
-                                              0, 0);
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{v16[2], v16[3]}, ro,
-                                              off + 8, 0, 0);
-      }
-    }
-    if (a.lse) {
-      const auto rl = __builtin_amdgcn_make_buffer_rsrc(
-          a.lse + (int64_t)f.head * lse_rows + f.t0 + f.qrow0, (short)0,
-          4 * nrow, 0x00020000);
-      __builtin_amdgcn_raw_buffer_store_b32(
-          __builtin_bit_cast(uint32_t, lse_v), rl, h2 == 0 ? 4 * l32 : 0x40000000,
-          0, 0);
-    }
-    return (al16 ? 8 : 16) + (a.lse ? 1 : 0);
-  };
-
-  Work wk{};
-  if (w == 0) wk = find_work(claim());
-  wk = hand_over(wk);
-  if (wk.seq >= 0 && !rejected) load_q(wk);
-  while (wk.seq >= 0) {
-    const int lane = opaque(tid & 63), l32 = lane & 31, h2 = lane >> 5;
-    const int kvh = wk.kvh;
-    const int seq = wk.seq;
-    const int qb = wk.qb;
-
-    const int t0 = wk.t0;
-    const int len = wk.len;
-    const int q0 = qb * BQ;
-    const int prior = wk.prior;
-    const int nk = prior + len;                 // keys of this run
-    const int qn = min(BQ, len - q0);
-    const int pos_lo = prior + q0;              // first query position
-    const int pos_hi = prior + q0 + qn - 1;     // last valid query position
-    // first key any query of the block may see; tiles start at a multiple of
-    // the tile width below it
-    const int kwin = a.window > 0 ? max(0, pos_lo - a.window + 1) : 0;
-    const int k_lo = (kwin / kBN) * kBN;
-    const int k_hi = pos_hi + 1;                // exclusive
-    const int ntiles = (k_hi - k_lo + kBN - 1) / kBN;
-
-    // ---- this wave's row block: head and 32-query sub-block ----------------
-    const int head = kvh * REP + w / QSUB;
-    const int qi = q0 + 32 * (w % QSUB) + l32;  // this lane's query (column)
-    const bool qok = qi < len;
-    const int qpos = prior + qi;
-
-    // ---- tile loads: global -> LDS directly (buffer_load ... lds) ----------
-    // Wave w moves key rows 4w..4w+3 and 32+4w..32+4w+3 of the K and the V
-    // tile: one 1 KB instruction per 4 rows, lane l writing LDS bytes
-    // 16l..16l+15 of the 4-row block, i.e. row l>>4, physical 16-byte slot
-    // l&15. The lane fetches the logical chunk that belongs in that slot:
-    // K: slot c ^ (row & 15); V: 64-byte block b ^ (row & 3).
-    // Rows past the run end (and pages outside the pool) fall outside the
-    // buffer resource and arrive as zeros; tile offsets ride in the lane
-    // offset, which is what the hardware range-checks.
-    const int grp = lane >> 4, slot = lane & 15;
-    const int kchunk = slot ^ ((4 * w + grp) & 15);
-    const int vchunk = ((((slot >> 2) ^ grp) & 3) << 2) | (slot & 3);
-    // packed rows of the run (keys 0.. of the run itself)
-    auto rk = mk_rsrc<VIS>(nullptr, 0u), rv = mk_rsrc<VIS>(nullptr, 0u);
-    int kst_b = 0, vst_b = 0, klane_p = 0, vlane_p = 0;
-    if constexpr (OWN) {
-      kst_b = (int)(a.k_st * 2);
-      vst_b = (int)(a.v_st * 2);
-      rk = mk_rsrc<VIS>(a.k + (int64_t)t0 * a.k_st + (int64_t)kvh * a.k_sh,
-                        (uint32_t)(((int64_t)(len - 1) * a.k_st + kD) * 2));
-      rv = mk_rsrc<VIS>(a.v + (int64_t)t0 * a.v_st + (int64_t)kvh * a.v_sh,
-                        (uint32_t)(((int64_t)(len - 1) * a.v_st + kD) * 2));
-      klane_p = grp * kst_b + 16 * kchunk;
-      vlane_p = grp * vst_b + 16 * vchunk;
-    }
-    // pool rows: keys below `plim` (all keys on the paged source, the prior
-    // context on the mixed one)
-    [[maybe_unused]] const int row_b = a.HKV * kD * 2;   // one token row
-    [[maybe_unused]] const int64_t page_b = (int64_t)kPage * row_b;
-    [[maybe_unused]] int klane = 0, vlane = 0;
-    if constexpr (POOL) {
-      klane = grp * row_b + kvh * (kD * 2) + 16 * kchunk;
-      vlane = grp * row_b + kvh * (kD * 2) + 16 * vchunk;
-    }
-    [[maybe_unused]] const int32_t __attribute__((address_space(4)))* trow =
-        POOL ? as_const(a.bt) + (int64_t)seq * a.bt_stride : nullptr;
-    [[maybe_unused]] const int plim = SRC == kMixed ? prior : nk;
-
-    // Four pool rows key0..key0+3 (one page: key0 % 4 == 0) into LDS. The
-    // buffer resource covers only the page's rows in [kwin, plim): rows before
-    // the first key a query of the block may see and rows past the pool's
-    // part read as zeros and are never fetched (a ring page there holds an
-    // overwritten position, a windowed table may point it at a poison page),
-    // and so does a page whose table entry lies outside the pool or past the
-    // row's width. The lane offset is relative to the resource base, so the
-    // rows below it have negative offsets, i.e. out of range.
-    auto pool_dma = [&](int key0, uint32_t dk, uint32_t dv) {
-      if constexpr (POOL) {
-        const int lp = key0 >> 4;
-        const int col = a.table_wrap > 0 ? lp % a.table_wrap : lp;
-        const int pg = (unsigned)col < (unsigned)a.bt_width ? trow[col] : -1;
-        const int r_lo = min(kPage, max(0, kwin - kPage * lp));
-        const int r_hi = min(kPage, max(0, plim - kPage * lp));
-        const bool valid = (unsigned)pg < (unsigned)a.num_pages && r_hi > r_lo;
-        const uint32_t nrec = valid ? (uint32_t)((r_hi - r_lo) * row_b) : 0u;
-        const int64_t pofs = valid ? (int64_t)pg * page_b + r_lo * row_b : 0;
-        const int roff = ((key0 & (kPage - 1)) - r_lo) * row_b;
-        dma(mk_rsrc<VIS>(reinterpret_cast<const char*>(a.kpool) + pofs,
-                              nrec),
-                 dk, klane + roff);
-        dma(mk_rsrc<VIS>(reinterpret_cast<const char*>(a.vpool) + pofs,
-                              nrec),
-                 dv, vlane + roff);
-      }
-    };
-    // four packed rows j..j+3 of the run's own keys into LDS (rows past the
-    // run end are outside the resource: zeros)
-    auto own_dma = [&](int j, uint32_t dk, uint32_t dv) {
-      if constexpr (OWN) {
-        dma(rk, dk, klane_p + j * kst_b);
-        dma(rv, dv, vlane_p + j * vst_b);
-      }
-    };
-
-    // issue tile `t` (index from k_lo) into LDS stage `st`: 4 instructions
-    // per wave (2 with the source split inside a 4-row block: one per source,
-    // each under the exec mask of the lanes whose row it holds)
-    auto issue_tile = [&](int t, int st) {
-      const int kt = k_lo + t * kBN;
-      const uint32_t sb = lds0 + st * kStage;
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int r0 = 4 * w + 32 * i;          // first row of the block
-        const uint32_t dk = sb + r0 * kRowB, dv = dk + kTileB;
-        const int key0 = kt + r0;
-        if constexpr (SRC == kPacked) {
-          own_dma(key0, dk, dv);
-        } else if constexpr (SRC == kPaged) {
-          pool_dma(key0, dk, dv);
-        } else {
-          if (key0 + 4 <= plim) {
-            pool_dma(key0, dk, dv);
-          } else if (key0 >= plim) {
-            own_dma(key0 - plim, dk, dv);
-          } else {
-            // lane group grp holds row key0 + grp
-            if (key0 + grp < plim) pool_dma(key0, dk, dv);
-            else own_dma(key0 - plim, dk, dv);
-          }
-        }
-      }
-    };
-
-    // ---- LDS fragment addresses -------------------------------------------
-    // K fragment (kb, kk) of lane (l32, h2): row 32 kb + l32, logical chunk
-    // 2 kk + h2 -> slot (2 kk + h2) ^ (l32 & 15) = (h2 ^ (l32 & 15)) ^ 2 kk.
-    const uint32_t ka0 = (uint32_t)(l32 * kRowB + 16 * (h2 ^ (l32 & 15)));
-    // V^T fragment (db, kb, kk) by two transposed reads: within each 16-lane
-    // group, source lane s names key kbase + (s >> 2), dims 4 (s & 3)..+3 of
-    // a 16-dim half; lane i of the group then holds dim dbase + i of keys
-    // kbase..kbase+3. kbase = 32 kb + 16 kk + 4 h2 (+8 for the second read),
-    // dbase = 32 db + 16 (l32 >> 4), which matches the order of this lane's
-    // probabilities (keys 16 kk + 4 h2 + 0..3 and 16 kk + 8 + 4 h2 + 0..3).
-    const int s16 = lane & 15;
-    const uint32_t va0 = (uint32_t)((4 * h2 + (s16 >> 2)) * kRowB +
-                                    64 * (s16 >> 2) + 32 * ((lane >> 4) & 1) +
-                                    8 * (s16 & 3));
-
-    // S^T = K.Q^T for the tile in `stage` (keys on M, queries on N)
-    auto scores = [&](int stage, f32x16 (&s)[2]) {
-      const uint32_t kb0 = ka0 + lds0 + stage * kStage;
-      s[0] = f32x16{};
-      s[1] = f32x16{};
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk)
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          const bf16x8 kf = lds_ld128((kb0 ^ (32u * kk)) + 32 * kb * kRowB);
-          s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kb], 0,
-                                                          0, 0);
-        }
-    };
-
-    // V^T fragment (db, kb, kk) of the tile whose V rows start at vbase
-    auto vfrag = [&](uint32_t vdb, int kb, int kk) {
-      const uint32_t p = vdb + (32 * kb + 16 * kk) * kRowB;
-      const bf16x4 lo = lds_tr16(p);
-      const bf16x4 hi = lds_tr16(p + 8 * kRowB);
-      return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-    };
-
-    // Fused bias rows of this wave's 32 queries: one buffer resource from
-    // the first query's row (lane offsets: row l32, 32-bit), covering the
-    // rows of the run only, so reads past them return zeros.
-    // (The resource starts at the dword holding that row's first value and
-    // ends at the dword holding the last row's last value, so that the dword
-    // loads below are aligned whatever the strides and every dword holding a
-    // value of the rows is in range.)
-    const int rel_row0 = q0 + 32 * (w % QSUB);
-    const int rel_nrow = REL ? min(32, len - rel_row0) : 0;
-    const char* const rel_first =
-        REL ? reinterpret_cast<const char*>(a.rel + (int64_t)(t0 + rel_row0) *
-                                                        a.r_st +
-                                            (int64_t)head * a.r_sh)
-            : nullptr;
-    const int rel_mis = (int)((uintptr_t)rel_first & 3);   // 0 or 2
-    [[maybe_unused]] const __amdgpu_buffer_rsrc_t rrel =
-        __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<char*>(rel_first - rel_mis), (short)0,
-            rel_nrow > 0 ? ((int)(((int64_t)(rel_nrow - 1) * a.r_st +
-                                   a.rel_extent) * 2) + rel_mis + 3) & ~3
-                         : 0,
-            0x00020000);
-    [[maybe_unused]] const int rrow_b =
-        REL ? rel_mis + l32 * (int)(a.r_st * 2) : 0;
-
-    // The fused bias of a key tile, loaded one softmax ahead (bias_issue)
-    // and applied in the softmax (bias_apply). The lane's keys come in runs
-    // of four (key0 .. key0+3, dist d0 .. d0-3), whose four bf16 values are
-    // adjacent in the row: the three dwords from the one holding rel[d0-3],
-    // realigned by 0 or 2 bytes. The range check is per dword and the
-    // resource ends at a dword boundary, so every value of the rows arrives;
-    // the whole offset goes in the lane register, where the check sees it.
-    // Every call issues exactly 8 loads (a tile outside the band or past the
-    // run reads nothing), so the wave's load counts stay fixed: the waits
-    // for them never reach the tile DMA issued after them.
-    typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-    [[maybe_unused]] u32x3 rb[8];
-    [[maybe_unused]] auto bias_issue = [&](int kt) {
-      if constexpr (REL) {
-        const bool band_tile =
-            kt < k_hi && pos_lo - (kt + kBN - 1) < a.rel_extent;
-        // byte offset of rel[d0 - 3] for kb = g = 0, opaque to the compiler
-        // so that the eight offsets are derived from it here rather than
-        // hoisted out of the key loop as eight live registers
-        int base = rrow_b + 2 * (qpos - kt - 4 * h2 - 3);
-        asm volatile("" : "+v"(base));
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int b4 = (base - 64 * kb - 16 * g) & ~3;
-            // before the first row (row 0 near dist 0): from the row start,
-            // shifted back into place by bias_apply
-            int off = band_tile ? (b4 < 0 ? 0 : b4) : 0x7ffffff0;
-            asm volatile("" : "+v"(off));
-            rb[4 * kb + g] = __builtin_bit_cast(
-                u32x3, __builtin_amdgcn_raw_buffer_load_b96(rrel, off, 0, 0));
-          }
-      }
-    };
-    // the scores move to the log2 domain: s*scale*log2e + rel*log2e,
-    // rel[q, h, dist] for 0 <= dist < E, zero outside
-    // Byte shift that realigns a lane's runs: the same on every tile (tile
-    // starts are multiples of 64 keys, so only the row's parity matters).
-    [[maybe_unused]] const uint32_t rel_sh =
-        REL ? (uint32_t)((rrow_b + 2 * (qpos - 3)) & 3) : 0u;
-    // The scores of a bias tile move to the natural-log domain with the bias
-    // added: s*scale + rel[q, h, dist] for 0 <= dist < E, zero outside.
-    // FAST (a whole tile with every dist in [0, E) for every query: no mask,
-    // no band test, every run starts inside its row) costs two byte-aligns
-    // per run and two instructions per score; the checked path handles the
-    // tiles at the diagonal, the run ends and the band edge.
-    [[maybe_unused]] auto bias_apply = [&](f32x16 (&s)[2], int kt,
-                                           auto fast_c) {
-      constexpr bool fast = decltype(fast_c)::value;
-      if constexpr (REL) {
-        // dist of the lane's first key for kb = g = 0 (opaque, as above)
-        int dq = qpos - kt - 4 * h2;
-        asm volatile("" : "+v"(dq));
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int d0 = dq - 32 * kb - 8 * g;
-            const uint32_t x0 = rb[4 * kb + g][0], x1 = rb[4 * kb + g][1],
-                           x2 = rb[4 * kb + g][2];
-            uint32_t w0, w1;
-            if constexpr (fast) {
-              w0 = __builtin_amdgcn_alignbyte(x1, x0, rel_sh);
-              w1 = __builtin_amdgcn_alignbyte(x2, x1, rel_sh);
-            } else {
-              const int b = rrow_b + 2 * (d0 - 3);
-              const int b4 = b & ~3;
-              // dwords the load started after the one holding rel[d0-3]
-              // (only when that one lies before the row; 3 or more: every
-              // dist of the run is negative, i.e. masked)
-              const int kd = b4 < 0 ? (-b4) >> 2 : 0;
-              const uint32_t y0 = kd == 0 ? x0 : 0u;
-              const uint32_t y1 = kd == 0 ? x1 : (kd == 1 ? x0 : 0u);
-              const uint32_t y2 = kd == 0 ? x2 : (kd == 1 ? x1 : x0);
-              w0 = __builtin_amdgcn_alignbyte(y1, y0, rel_sh);
-              w1 = __builtin_amdgcn_alignbyte(y2, y1, rel_sh);
-            }
-            // element 4g + i is key0 + i, dist d0 - i
-            const uint32_t hv[4] = {w1 & 0xffff0000u, w1 << 16,
-                                    w0 & 0xffff0000u, w0 << 16};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              float bias = __builtin_bit_cast(float, hv[i]);
-              if constexpr (!fast) {
-                const int dist = d0 - i;
-                const bool band = qok && dist >= 0 && dist < a.rel_extent;
-                bias = band ? bias : 0.0f;
-              }
-              s[kb][4 * g + i] =
-                  __builtin_fmaf(s[kb][4 * g + i], a.scale, bias);
-            }
-          }
-      }
-    };
-
-    // per-element mask: causal, window, run end. Element j of block kb holds
-    // key kt + 4 h2 + c with c = 32 kb + 8 (j >> 2) + (j & 3), a compile-time
-    // constant, and the keys a query sees form one interval lo < c <= hi per
-    // lane: two compares and a select per score.
-    auto mask_tile = [&](f32x16 (&s)[2], int kt) {
-      const int base = kt + 4 * h2;
-      const int hi = qok ? min(qpos, nk - 1) - base : -1;
-      const int lo = a.window > 0 ? qpos - a.window - base : -1;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int c = 32 * kb + 8 * (j >> 2) + (j & 3);
-          s[kb][j] = (c <= hi && c > lo) ? s[kb][j] : -INFINITY;
-        }
-    };
-
-    // ---- accumulators: carried in from the work-group scope, reset below,
-    // once the previous item's output has been stored ------------------------
-    // Without a bias the max runs on the raw scores (scale > 0 commutes with
-    // max) and each probability is one fma + exp2: p = 2^(s*scale*log2e - m).
-    // (on tiles that carry the fused bias the scores are s*scale + bias,
-    // and the factor is log2e)
-
-    // Lazy rescaling: the running max (log2 domain) only moves when the
-    // tile's max exceeds it by more than kLazy, so probabilities stay below
-    // 2^kLazy and O^T / l are rescaled on few tiles; O / l and the LSE are
-    // exact for any reference point.
-    auto new_max = [&](float mx, float sl2, bool& move, float& m_use) {
-      const auto sw = __builtin_amdgcn_permlane32_swap(
-          __builtin_bit_cast(uint32_t, mx), __builtin_bit_cast(uint32_t, mx),
-          false, false);
-      mx = fmaxf(__builtin_bit_cast(float, (uint32_t)sw[0]),
-                 __builtin_bit_cast(float, (uint32_t)sw[1]));
-      const float m_cand = mx * sl2;
-      move = m_cand > m_run + kLazy;
-      const float m_new = move ? m_cand : m_run;
-      m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float alpha = move ? fast_exp2(m_run - m_use) : 1.0f;
-      m_run = m_new;
-      return alpha;
-    };
-    // probability pair q (kb = q >> 3, kk = (q >> 2) & 1, e = q & 3)
-    auto prob_pair = [&](const f32x16 (&s)[2], int q, float sl2, float m_use,
-                         float& psum) {
-      const int kb = q >> 3, kk = (q >> 2) & 1, e = q & 3;
-      const float p0 =
-          fast_exp2(__builtin_fmaf(s[kb][8 * kk + 2 * e], sl2, -m_use));
-      const float p1 =
-          fast_exp2(__builtin_fmaf(s[kb][8 * kk + 2 * e + 1], sl2, -m_use));
-      psum += p0 + p1;
-      return pack_bf16x2_rn(p0, p1);
-    };
-    auto pack_p = [&](const uint32_t (&pw)[16], bf16x8 (&pf)[2][2]) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const int q = 8 * kb + 4 * kk;
-          pf[kb][kk] = __builtin_bit_cast(
-              bf16x8, u32x4{pw[q], pw[q + 1], pw[q + 2], pw[q + 3]});
-        }
-    };
-
-    // ---- two wave groups in ping-pong ---------------------------------------
-    // Waves 0-3 and 4-7 (one of each per SIMD) alternate between an MFMA
-    // phase (P.V of tile t and the scores of tile t+1: 32 MFMAs, fragment
-    // reads, hardly any VALU) and a softmax phase (the online softmax of those
-    // scores: VALU only), half a tile apart: while one wave of a SIMD keeps
-    // the matrix core busy the other one uses the vector ALU. A work-group
-    // barrier ends every phase (two per tile); group 1 runs one phase behind
-    // group 0 (its first softmax shares the slot of group 0's first
-    // multiply), and both pass the same barriers in the same order.
-    const int grp_id = w >> 2;
-    // A tile every valid query of the block sees whole. Query columns past
-    // the run end (a partial last block) are left unmasked there: their Q
-    // fragments are zero, so their scores are finite, and their rows are
-    // never stored (masking them sent every tile of such a block down the
-    // masked path, at about twice the cost per tile).
-    auto full_tile = [&](int kt) {
-      return (kt + kBN - 1 <= pos_lo) && (kt + kBN <= nk) &&
-             (a.window == 0 || pos_hi - kt < a.window);
-    };
-    f32x16 sc[2];        // scores of the tile after the one being multiplied
-    bf16x8 pf[2][2];     // probabilities of the tile being multiplied
-
-    // softmax of scores `s` of the tile at kt (masking when needed): P^T
-    // fragments, running max / sum update, O^T rescale when the max moved
-    auto softmax_phase = [&](f32x16 (&s)[2], int kt, bool first) {
-      // the bias band: some pair of the tile has dist = q - k < E (the
-      // smallest dist is pos_lo - (kt + 63))
-      const bool with_bias = REL && pos_lo - (kt + kBN - 1) < a.rel_extent;
-      const bool full = full_tile(kt);
-      if constexpr (REL) {
-        if (with_bias) {
-          if (full && pos_hi - kt < a.rel_extent)
-            bias_apply(s, kt, std::true_type{});
-          else
-            bias_apply(s, kt, std::false_type{});
-        }
-      }
-      if (!full) mask_tile(s, kt);
-      const float sl2 = with_bias ? kLog2e : a.scale_log2;
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 16; j += 2)
-          mx = fmaxf(fmaxf(mx, s[kb][j]), s[kb][j + 1]);
-      bool move;
-      float m_use;
-      const float alpha = new_max(mx, sl2, move, m_use);
-      float psum = 0.0f;
-      uint32_t pw[16];
-#pragma unroll
-      for (int q = 0; q < 16; ++q) pw[q] = prob_pair(s, q, sl2, m_use, psum);
-      pack_p(pw, pf);
-      l_part = l_part * alpha + psum;
-      // O^T holds the tiles before this one: rescale it to the new reference
-      // (in place, each product tied to its accumulator register: a plain
-      // multiply under the branch leaves the compiler a merge of two copies
-      // of O^T, which it resolves with 32 register-pair moves on every tile)
-      if (!first && __builtin_amdgcn_ballot_w64(move)) {
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-          for (int j = 0; j < 16; ++j) {
-            float x = o_acc[db][j];
-            asm volatile("v_mul_f32 %0, %1, %0" : "+v"(x) : "v"(alpha));
-            o_acc[db][j] = x;
-          }
-      }
-    };
-
-    // MFMA phase of tile t: O^T += V^T.P^T for tile t (four accumulators in
-    // turn) interleaved with the scores of tile t+1 (two accumulators), the
-    // V^T and K fragments read kRing - 1 MFMAs ahead (3: measured ~1% over 4
-    // and 5 ahead on 4K-16K runs)
-    auto mfma_phase = [&](int t, auto with_s_c) {
-      // (with_s as a type: one straight-line copy per case, no branch between
-      // the MFMAs)
-      constexpr bool with_s = decltype(with_s_c)::value;
-      // the SIMD's issue port goes to this wave's MFMAs first; the softmax
-      // wave fills the slots in between (measured ~2% over equal priority)
-      __builtin_amdgcn_s_setprio(1);
-      const uint32_t vb = va0 + lds0 + (t & 3) * kStage + kTileB;
-      const uint32_t kb0 = ka0 + lds0 + ((t + 1) & 3) * kStage;
-      auto vf_n = [&](int n) {
-        const int db = n & 3, kb = n >> 3, kk = (n >> 2) & 1;
-        return vfrag(vb ^ (64u * db), kb, kk);
-      };
-      auto kf_n = [&](int n) {
-        return lds_ld128((kb0 ^ (32u * (n >> 1))) + 32 * (n & 1) * kRowB);
-      };
-      // fragments read R - 1 MFMAs ahead (one fewer with the fused bias,
-      // whose prefetched values take the registers)
-      constexpr int R = REL ? kRing - 1 : kRing;
-      bf16x8 vf[R], kf[R];
-#pragma unroll
-      for (int i = 0; i < R - 1; ++i) {
-        vf[i] = vf_n(i);
-        if (with_s) kf[i] = kf_n(i);
-      }
-#pragma unroll
-      for (int n = 0; n < 16; ++n) {
-        if (n + R - 1 < 16) vf[(n + R - 1) % R] = vf_n(n + R - 1);
-        if (with_s && n + R - 1 < 16) kf[(n + R - 1) % R] = kf_n(n + R - 1);
-        const int db = n & 3, kb = n >> 3, kk = (n >> 2) & 1;
-        o_acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            vf[n % R], pf[kb][kk], o_acc[db], 0, 0, 0);
-        if (with_s) {
-          const int skb = n & 1, skk = n >> 1;
-          sc[skb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              kf[n % R], qf[skk], n < 2 ? f32x16{} : sc[skb], 0, 0, 0);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      __builtin_amdgcn_s_setprio(0);
-    };
-
-    // this wave's queries (loaded at the end of the previous item)
-    if (!rejected) {
-      wait_vm<0>();
-      read_q();
-    }
-    // The ticket of the item after this one is claimed about three tiles
-    // before this item ends (by the leader, in group 0's tile loop): late
-    // enough that tickets go out in the order the work-groups finish, as a
-    // dispatcher would hand them out, which keeps the heaviest-first order
-    // when there are few items per CU; early enough that the atomic's
-    // latency is hidden.
-    int nxt = 0;
-    const int claim_t = max(0, ntiles - 4);
-    if (leader && (rejected || ntiles == 1)) nxt = atomicAdd(ctr + x, 1);
-    // ---- pipeline: 4 LDS stages, tiles issued three ahead -------------------
-    // Slot 2t: group 0 multiplies tile t, group 1 does the softmax of tile t;
-    // slot 2t+1: group 0 the softmax of tile t+1, group 1 multiplies tile t.
-    // Tile t+3 goes out at the start of slot 2t into the stage of tile t-1
-    // (last read in slot 2t-1) and must be in LDS before slot 2t+4; each
-    // wave waits for its own part at the end of every odd slot, before the
-    // barrier that publishes it (4 instructions per wave per tile).
-    // Tiles 0 and 1 go into stages 0 and 1 while the previous item's output
-    // goes out through stages 2 and 3.
-    if (!rejected) {
-      issue_tile(0, 0);
-      if (ntiles > 1) issue_tile(1, 1);
-    }
-    // the previous item's rows go out now; wait for everything issued
-    // before them
-    if (have_prev) prev_lse = stage_output();
-    const int nst = have_prev ? flush_output(prev, prev_lse) : 0;
-    if (nst == 17) wait_vm<17>();
-    else if (nst == 16) wait_vm<16>();
-    else if (nst == 9) wait_vm<9>();
-    else if (nst == 8) wait_vm<8>();
+  for (int kk = 0; kk < 8; ++kk) {
+    u32x4 x = __builtin_bit_cast(
+        u32x4,
+        lds_ld128(qlds + l32 * kRowB + 16 * ((2 * kk + h2) ^ (l32 & 15))));
+    if (!qok) x = u32x4{0, 0, 0, 0};
+    qf[kk] = __builtin_bit_cast(bf16x8, x);
+  }
+  __syncthreads();
+  if (ntiles > 2) issue_tile(2, 2);
+  // End of every odd slot: this wave's part of tile t+2 must be in LDS
+  // before the barrier that publishes it. Loads issued after that tile's
+  // may still fly: the DMA of tile t+3 and, with the fused bias, the bias
+  // loads of the tile after the next softmax (`bias` of them).
+  auto odd_end = [&](int t, int bias) {
+    const int n = (t + 3 < ntiles ? 4 : 0) + bias;
+    if (n == 12) wait_vm<12>();
+    else if (n == 8) wait_vm<8>();
+    else if (n == 4) wait_vm<4>();
     else wait_vm<0>();
     __syncthreads();
+  };
+  constexpr int NB = REL ? 8 : 0;   // bias loads per tile
+  // The first and last tiles are peeled off the loops, so that the loops
+  // hold one variant of the MFMA phase: O^T then keeps one set of
+  // registers across iterations (variants merged inside the loop made the
+  // compiler copy all 64 accumulator registers back and forth every tile).
+  constexpr std::true_type kWithS{};
+  constexpr std::false_type kNoS{};
+  if (grp_id == 0) {
+    scores(0, sc);
+    bias_issue(k_lo);
+    softmax_phase(sc, k_lo, true);
+    bias_issue(k_lo + kBN);
+    for (int t = 0; t + 1 < ntiles; ++t) {
+      if (t + 3 < ntiles) issue_tile(t + 3, (t + 3) & 3);
+      mfma_phase(t, kWithS);
+      __syncthreads();
+      softmax_phase(sc, k_lo + (t + 1) * kBN, false);
+      bias_issue(k_lo + (t + 2) * kBN);
+      odd_end(t, NB);
+    }
+    mfma_phase(ntiles - 1, kNoS);
+    __syncthreads();
+    odd_end(ntiles - 1, 0);
+  } else {
+    if (3 < ntiles) issue_tile(3, 3);
+    scores(0, sc);
+    bias_issue(k_lo);
+    softmax_phase(sc, k_lo, true);
+    bias_issue(k_lo + kBN);
+    __syncthreads();
+    if (ntiles > 1) mfma_phase(0, kWithS);
+    else mfma_phase(0, kNoS);
+    odd_end(0, NB);
+    for (int t = 1; t + 1 < ntiles; ++t) {
+      if (t + 3 < ntiles) issue_tile(t + 3, (t + 3) & 3);
+      softmax_phase(sc, k_lo + t * kBN, false);
+      bias_issue(k_lo + (t + 1) * kBN);
+      __syncthreads();
+      mfma_phase(t, kWithS);
+      odd_end(t, NB);
+    }
+    if (ntiles > 1) {
+      const int t = ntiles - 1;
+      softmax_phase(sc, k_lo + t * kBN, false);
+      bias_issue(k_lo + (t + 1) * kBN);
+      __syncthreads();
+      mfma_phase(t, kNoS);
+      odd_end(t, NB);
+    }
+  }
+  }  // !rejected
+
+  // ---- finalise: l over both lane halves, normalise, store --------------
+  const float l_tot = l_part + __shfl_xor(l_part, 32);
+  const float inv = rejected ? __builtin_nanf("") :
+                    l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+  if (a.lse && h2 == 0 && qok)
+    a.lse[(int64_t)head * wk.total + t0 + qi] =
+        rejected ? __builtin_nanf("") :
+        l_tot > 0.0f ? (m_run + fast_log2(l_tot)) * kLn2 : -INFINITY;
+  // O^T goes through LDS (free after the last barrier) so that the global
+  // stores are whole rows: the wave writes its 32 x 128 block query-major
+  // (256-byte rows, 16-byte chunks swizzled by row & 15, so neither the
+  // 8-byte writes nor the 16-byte reads conflict), then each store
+  // instruction covers 4 complete rows (16 lanes x 16 bytes per row)
+  // instead of 16 bytes of 32 rows.
+  const uint32_t ob = lds0 + (uint32_t)w * (32 * kRowB);
 #pragma unroll
-    for (int db = 0; db < 4; ++db) o_acc[db] = f32x16{};
-    m_run = -INFINITY;
-    l_part = 0.0f;
-    if (!rejected) {
-    if (ntiles > 2) issue_tile(2, 2);
-    // End of every odd slot: this wave's part of tile t+2 must be in LDS
-    // before the barrier that publishes it. Loads issued after that tile's
-    // may still fly: the DMA of tile t+3 and, with the fused bias, the bias
-    // loads of the tile after the next softmax (`bias` of them).
-    auto odd_end = [&](int t, int bias) {
-      const int n = (t + 3 < ntiles ? 4 : 0) + bias;
-      if (n == 12) wait_vm<12>();
-      else if (n == 8) wait_vm<8>();
-      else if (n == 4) wait_vm<4>();
-      else wait_vm<0>();
-      __syncthreads();
-    };
-    constexpr int NB = REL ? 8 : 0;   // bias loads per tile
-    // The first and last tiles are peeled off the loops, so that the loops
-    // hold one variant of the MFMA phase: O^T then keeps one set of
-    // registers across iterations (variants merged inside the loop made the
-    // compiler copy all 64 accumulator registers back and forth every tile).
-    constexpr std::true_type kWithS{};
-    constexpr std::false_type kNoS{};
-    if (grp_id == 0) {
-      scores(0, sc);
-      bias_issue(k_lo);
-      softmax_phase(sc, k_lo, true);
-      bias_issue(k_lo + kBN);
-      for (int t = 0; t + 1 < ntiles; ++t) {
-        if (leader && t == claim_t) nxt = atomicAdd(ctr + x, 1);
-        if (t + 3 < ntiles) issue_tile(t + 3, (t + 3) & 3);
-        mfma_phase(t, kWithS);
-        __syncthreads();
-        softmax_phase(sc, k_lo + (t + 1) * kBN, false);
-        bias_issue(k_lo + (t + 2) * kBN);
-        odd_end(t, NB);
-      }
-      mfma_phase(ntiles - 1, kNoS);
-      __syncthreads();
-      odd_end(ntiles - 1, 0);
-    } else {
-      if (3 < ntiles) issue_tile(3, 3);
-      scores(0, sc);
-      bias_issue(k_lo);
-      softmax_phase(sc, k_lo, true);
-      bias_issue(k_lo + kBN);
-      __syncthreads();
-      if (ntiles > 1) mfma_phase(0, kWithS);
-      else mfma_phase(0, kNoS);
-      odd_end(0, NB);
-      for (int t = 1; t + 1 < ntiles; ++t) {
-        if (t + 3 < ntiles) issue_tile(t + 3, (t + 3) & 3);
-        softmax_phase(sc, k_lo + t * kBN, false);
-        bias_issue(k_lo + (t + 1) * kBN);
-        __syncthreads();
-        mfma_phase(t, kWithS);
-        odd_end(t, NB);
-      }
-      if (ntiles > 1) {
-        const int t = ntiles - 1;
-        softmax_phase(sc, k_lo + t * kBN, false);
-        bias_issue(k_lo + (t + 1) * kBN);
-        __syncthreads();
-        mfma_phase(t, kNoS);
-        odd_end(t, NB);
+  for (int db = 0; db < 4; ++db)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const uint32_t w0 = pack_bf16x2(f32_to_bf16_bits(o_acc[db][4 * g4] * inv),
+                                      f32_to_bf16_bits(o_acc[db][4 * g4 + 1] * inv));
+      const uint32_t w1 = pack_bf16x2(f32_to_bf16_bits(o_acc[db][4 * g4 + 2] * inv),
+                                      f32_to_bf16_bits(o_acc[db][4 * g4 + 3] * inv));
+      const int c = 4 * db + g4;    // 16-byte chunk: dims 8c .. 8c+7
+      lds_st64(ob + l32 * kRowB + 16 * (c ^ (l32 & 15)) + 8 * h2,
+               u32x2{w0, w1});
+    }
+  wave_lds_sync();
+  const int qrow0 = q0 + 32 * (w % QSUB);   // query of the block's row 0
+  const int c16 = lane & 15;
+  const bool al16 = ((a.o_st | a.o_sh) & 7) == 0 &&
+                    ((uintptr_t)a.out & 15) == 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 4 * i + (lane >> 4);
+    const u32x4 x = __builtin_bit_cast(
+        u32x4, lds_ld128(ob + r * kRowB + 16 * (c16 ^ (r & 15))));
+    if (qrow0 + r < len) {
+      __bf16* const dst = a.out + (int64_t)(t0 + qrow0 + r) * a.o_st +
+                          (int64_t)head * a.o_sh + 8 * c16;
+      if (al16) {
+        *reinterpret_cast<u32x4*>(dst) = x;
+      } else {
+        reinterpret_cast<u32x2*>(dst)[0] = u32x2{x[0], x[1]};
+        reinterpret_cast<u32x2*>(dst)[1] = u32x2{x[2], x[3]};
       }
     }
-    }  // !rejected
-    Work nw{};
-    if (w == 0) nw = find_work(__builtin_amdgcn_readfirstlane(nxt));
-    nw = hand_over(nw);
-    if (nw.seq >= 0 && !rejected) load_q(nw);
-    prev = Fin{head, t0, len, q0 + 32 * (w % QSUB)};
-    have_prev = true;
-    wk = nw;
-  }
-  if (have_prev) {
-    prev_lse = stage_output();
-    flush_output(prev, prev_lse);
-  }
-  // The last work-group out clears the counters for the next launch on this
-  // slot: every other work-group has had its last ticket before it counts
-  // itself done.
-  if (leader && atomicAdd(ctr + 8, 1) == (int)gridDim.x - 1) {
-#pragma unroll
-    for (int i = 0; i < 9; ++i) atomicExch(ctr + i, 0);
   }
 }
 
@@ -1154,57 +932,16 @@ void launch_src(const PrefillArgs& a, int src, dim3 grid, size_t lds,
                        lds, st, a);
 }
 
-// ---- ticket counters of the persistent grid -------------------------------
-// kSchedSlots slots of 16 ints per GPU (ticket counters of the 8 XCDs and a
-// done counter), zero when the library loads; each launch takes the next
-// slot in turn and its last work-group clears it again. Two launches that
-// share a slot must not run at the same time, which needs kSchedSlots
-// prefill launches in flight at once on one GPU.
-constexpr int kSchedSlots = 256;
-static __device__ __align__(256) int sched_slots[kSchedSlots * 16];
-
-constexpr int kMaxDevices = 64;
-std::mutex g_sched_mu;
-int* g_sched_addr[kMaxDevices] = {};
-std::atomic<unsigned> g_sched_next{0};
-
-// This launch's slot on the current device. The array's name is a host-side
-// stand-in in host code: its device address is resolved once per device,
-// with that device current, and only that address reaches the kernel.
-int sched_slot(int** slot) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
-  TMOPT_REQUIRE(e == hipSuccess && dev >= 0 && dev < kMaxDevices,
-                TMOPT_ELAUNCH, "prefill: no current device (%s)",
-                hipGetErrorString(e));
-  int* base;
-  {
-    std::lock_guard<std::mutex> lock(g_sched_mu);
-    if (g_sched_addr[dev] == nullptr) {
-      void* p = nullptr;
-      e = hipGetSymbolAddress(&p, HIP_SYMBOL(sched_slots));
-      TMOPT_REQUIRE(e == hipSuccess && p != nullptr, TMOPT_ELAUNCH,
-                    "prefill: hipGetSymbolAddress failed on device %d: %s",
-                    dev, hipGetErrorString(e));
-      g_sched_addr[dev] = static_cast<int*>(p);
-    }
-    base = g_sched_addr[dev];
-  }
-  *slot = base + 16 * (int)(g_sched_next.fetch_add(1) % kSchedSlots);
-  return TMOPT_OK;
-}
-
 template <int REP>
 void launch(PrefillArgs a, int src, int S, int max_seqlen, hipStream_t st) {
   constexpr int BQ = 256 / REP;
   a.nqb_max = (max_seqlen + BQ - 1) / BQ;
-  // one work-group per compute unit (the LDS stages take most of a CU),
-  // fewer when there are fewer items
-  const int64_t items = (int64_t)a.HKV * S * a.nqb_max;
-  const int cus = device_cus();
-  const dim3 grid((unsigned)(items < cus ? items : cus));
-  // the four stages, the item handed over and the run table
-  const size_t lds = kNStage * kStage + 32 + 3 * 256;
+  // HKV * items-per-head work-groups, rounded up to whole XCD rounds
+  const int64_t items = (int64_t)S * a.nqb_max;
+  int64_t n = a.HKV * items;
+  if (a.HKV <= 8 && 8 % a.HKV == 0) n = 8 * ((items + 8 / a.HKV - 1) / (8 / a.HKV));
+  const dim3 grid((unsigned)n);
+  const size_t lds = kNStage * kStage;
   if (a.rel)
     launch_src<REP, true>(a, src, grid, lds, st);
   else
@@ -1336,10 +1073,6 @@ extern "C" int tmopt_attn_prefill_varlen(
   TMOPT_REQUIRE(((int64_t)max_seqlen_q * q_stride_tok + kD) * 2 < (1ll << 31),
                 TMOPT_EUNSUPPORTED,
                 "prefill: a run's q span must stay below 2 GiB");
-  TMOPT_REQUIRE((32 * o_stride_tok + kD) * 2 < (1ll << 31) &&
-                    o_stride_tok >= 0 && o_stride_head >= 0,
-                TMOPT_EUNSUPPORTED,
-                "prefill: 32 output rows must span less than 2 GiB");
   TMOPT_REQUIRE(q_stride_tok % 8 == 0 && q_stride_head % 8 == 0 &&
                     o_stride_tok % 4 == 0 && o_stride_head % 4 == 0 &&
                     (uintptr_t)q % 16 == 0 && (uintptr_t)out % 8 == 0,
@@ -1379,8 +1112,6 @@ extern "C" int tmopt_attn_prefill_varlen(
   a.r_sh = rel_stride_head;
   a.rel_extent = rel ? rel_extent : 0;
   a.reject = reject;
-  const int rc = sched_slot(&a.sched);
-  if (rc != TMOPT_OK) return rc;
   hipStream_t st = (hipStream_t)stream;
   if (rep == 8)
     launch<8>(a, src, num_seqs, max_seqlen_q, st);

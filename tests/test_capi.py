@@ -127,3 +127,49 @@ def test_python_wrapper_asserts_before_launch(tm):
 def test_missing_library_fails_loudly(tm, tmp_path):
     with pytest.raises(tm.TmoptLibraryMissing):
         tm._lib.load(str(tmp_path / "absent.so"))
+
+
+C_CALLER = r"""
+#include <stdio.h>
+#include <string.h>
+#include "tmopt_attn.h"
+
+/* A C caller of the boundary, as the reference's C++ launcher would be:
+   sizes a decode workspace and gets status codes back for invalid calls,
+   without a GPU (validation returns before any HIP call). */
+int main(void) {
+  size_t ws = tmopt_attn_decode_workspace_size(64, 32, 4, 128, 0);
+  int rc = tmopt_attn_prefill_varlen(
+      NULL, 0, 0, NULL, 0, 0, NULL, 0, 0, NULL, NULL, 1, 16, NULL, NULL,
+      NULL, 0, 0, 16, 0, 32, 4, 128, 0, 0.1f, NULL, 0, 0, 0, NULL, 0, 0,
+      NULL, NULL, NULL);
+  printf("%s|%zu|%d|%s\n", tmopt_version(), ws, rc, tmopt_last_error());
+  return rc == TMOPT_EINVAL && ws > 0 &&
+         strstr(tmopt_last_error(), "null") != NULL ? 0 : 1;
+}
+"""
+
+
+def test_c_program_links_and_calls(tm, tmp_path):
+    """The header compiles as strict C99 and a C program links against the
+    built library and calls it (no Python in between)."""
+    import shutil
+    import subprocess
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc unavailable")
+    src = tmp_path / "caller.c"
+    src.write_text(C_CALLER)
+    exe = tmp_path / "caller"
+    libdir = os.path.dirname(tm._lib.LIB_PATH)
+    cc = subprocess.run(
+        ["gcc", "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror",
+         "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe),
+         "-L", libdir, "-ltmopt_attn", f"-Wl,-rpath,{libdir}"],
+        capture_output=True, text=True)
+    assert cc.returncode == 0, cc.stderr
+    run = subprocess.run([str(exe)], capture_output=True, text=True,
+                         timeout=120)
+    assert run.returncode == 0, run.stdout + run.stderr
+    version, ws, rc, msg = run.stdout.strip().split("|", 3)
+    assert version == tm.version()
+    assert int(ws) > 0 and int(rc) == tm._lib.TMOPT_EINVAL

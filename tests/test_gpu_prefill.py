@@ -207,6 +207,35 @@ def test_config4_sampled_rows(tm, dev, make, window):
                              f"C4 w={window} seq{i} q{j}")
 
 
+def test_one_long_run_sampled_rows(tm, dev):
+    """One run of 131,069 tokens (a long-context prompt; not a multiple of
+    the 32-query block or the 64-key tile), global: 4,096 key tiles for the
+    last query blocks, 16,384 work-groups. The oracle checks sampled rows
+    (first, last, tile and block edges, random) per KV-head group in
+    fp32."""
+    T = 131069
+    case = _wl().make_prefill("long1", 28, lens=[T], window=0, device=dev)
+    out, lse = tm.prefill_varlen(case.q, case.k, case.v, case.cu_seqlens,
+                                 case.scale, max_seqlen=T)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    K = case.k.float().cpu()                    # [T, HKV, D]
+    V = case.v.float().cpu()
+    HQ, HKV = case.q.shape[1], case.k.shape[1]
+    rep = HQ // HKV
+    g = torch.Generator().manual_seed(7)
+    rows = {0, 1, 31, 32, 63, 64, 4095, 65535, T - 33, T - 2, T - 1}
+    rows |= set(torch.randint(0, T, (5,), generator=g).tolist())
+    for j in sorted(rows):
+        qv = case.q[j].float().cpu().view(HKV, rep, -1)       # [HKV, rep, D]
+        s = torch.einsum("grd,ngd->grn", qv, K[:j + 1]) * case.scale
+        ref_l = torch.logsumexp(s, -1).reshape(HQ)
+        ref_o = torch.einsum("grn,ngd->grd", torch.softmax(s, -1),
+                             V[:j + 1]).reshape(HQ, -1)
+        assert_out_close(out[j].cpu(), ref_o, f"long run q{j}")
+        assert_lse_close(lse[:, j].cpu(), ref_l, f"long run q{j}")
+
+
 @pytest.mark.parametrize("E,window", [(95, 0), (1, 0), (80, 256), (300, 64)])
 @pytest.mark.parametrize("hq,hkv", [(32, 4), (64, 16)])
 def test_bias_band_shorter_than_runs(tm, dev, E, window, hq, hkv):

@@ -241,3 +241,37 @@ def test_row_width_bound(tm, dev):
                                              torch.tensor([64]), 0.1)
         assert_out_close(out[:1], ref_o, "row width")
         assert_lse_close(lse[:1], ref_l, "row width")
+
+
+@pytest.mark.parametrize("window", [0, 4096])
+def test_one_very_long_context(tm, dev, window):
+    """A 262,143-token context beside a 17-token one (NaN-poisoned pool
+    outside the backed pages): the long sequence is split over every
+    work-group of the persistent grid and merged from ~190 pieces. Checked
+    against an fp32 gather of its pages."""
+    from importlib import import_module
+    wl = import_module("tm-opt_amd.workloads")
+    ctx = [262143, 17]
+    case = wl.make_decode("long_ctx", 29, 2, 0, 0, window, device=dev,
+                          ctx=ctx)
+    out, lse = tm.decode_paged(case.q, case.k_pool, case.v_pool,
+                               case.block_table, case.ctx_lens, case.scale,
+                               window=window)
+    torch.cuda.synchronize()
+    out, lse = out.cpu(), lse.cpu()
+    HQ, HKV = case.q.shape[1], case.k_pool.shape[2]
+    rep = HQ // HKV
+    table = case.block_table.cpu().long()
+    for b, n in enumerate(ctx):
+        lo = max(0, n - window) if window else 0
+        pages = table[b, lo // 16:(n + 15) // 16].to(case.k_pool.device)
+        K = case.k_pool[pages].reshape(-1, HKV, 128)[lo % 16:][:n - lo]
+        V = case.v_pool[pages].reshape(-1, HKV, 128)[lo % 16:][:n - lo]
+        K, V = K.float().cpu(), V.float().cpu()
+        qv = case.q[b].float().cpu().view(HKV, rep, -1)
+        s = torch.einsum("grd,ngd->grn", qv, K) * case.scale
+        ref_l = torch.logsumexp(s, -1).reshape(HQ)
+        ref_o = torch.einsum("grn,ngd->grd", torch.softmax(s, -1),
+                             V).reshape(HQ, -1)
+        assert_out_close(out[b], ref_o, f"ctx {n} w={window}")
+        assert_lse_close(lse[b], ref_l, f"ctx {n} w={window}")

@@ -719,7 +719,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // MFMA phase of tile t: O^T += V^T.P^T for tile t (four accumulators in
   // turn) interleaved with the scores of tile t+1 (two accumulators), the
   // V^T and K fragments read kRing - 1 MFMAs ahead (3: measured ~1% over 4
-  // and 5 ahead on 4K-16K runs)
+  // and 5 ahead on 4K-16K runs; 2 with the fused bias)
   auto mfma_phase = [&](int t, auto with_s_c) {
     // (with_s as a type: one straight-line copy per case, no branch between
     // the MFMAs)
@@ -736,7 +736,10 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     auto kf_n = [&](int n) {
       return lds_ld128((kb0 ^ (32u * (n >> 1))) + 32 * (n & 1) * kRowB);
     };
-    constexpr int R = kRing;     // fragments read R - 1 MFMAs ahead
+    // fragments read R - 1 MFMAs ahead; one fewer with the fused bias, whose
+    // prefetched values need the registers (the fourth slot made the bias
+    // build spill: 2-3% slower on the adapters' shapes)
+    constexpr int R = REL ? kRing - 1 : kRing;
     bf16x8 vf[R], kf[R];
 #pragma unroll
     for (int i = 0; i < R - 1; ++i) {

@@ -470,10 +470,11 @@ class _BenchRing:
 def bench_prefill_append(tm, compat, sets, window, HKV, steps, warmup):
     """One prefill layer's cache population + attention, as the engine runs
     it (model.py:507-528), two ways: (a) the append of every row from the
-    sconv's channel-major K/V (tmopt_kv_write_paged reads them in place)
-    followed by attn_prefill_fused (packed copy of K/V + kernel); (b)
+    sconv's channel-major K/V (read in place) followed by
+    attn_prefill_fused (which reads the same K/V in place); (b)
     attn_prefill_fused given the caches (append inside; a global layer then
-    reads its keys from the pages: no copy). a - b is the copy removed."""
+    reads its keys from the pages just written, an SWA layer from the K/V
+    tensors). a - b is what the batched path removes."""
     q0, k0 = sets[0][0], sets[0][1]
     Bp, H, T, D = q0.shape
     npg = (T + 15) // 16
@@ -500,7 +501,8 @@ def bench_prefill_append(tm, compat, sets, window, HKV, steps, warmup):
 
     def separate(a):
         cs = caches(order[id(a)])
-        compat._append_rows(a[1], a[2], cs, [T] * Bp)
+        compat._append_rows(compat._kv_rows(a[1]), compat._kv_rows(a[2]), cs,
+                            [T] * Bp)
         compat.attn_prefill_fused(*a)
 
     def fused(a):
@@ -514,9 +516,10 @@ def bench_prefill_append(tm, compat, sets, window, HKV, steps, warmup):
     return {"ms_append_then_attention": ms_a,
             "ms_attention_with_caches": ms_b,
             "ms_removed": ms_a - ms_b,
-            "kv_copy_bytes_avoidable": kv_bytes * 2,
-            "note": "global: keys read back from the pages just written; "
-                    "SWA rings cannot hold T > W, so the packed copy stays"}
+            "kv_bytes_per_call": kv_bytes,
+            "note": "K/V channel-major, read in place by the append and "
+                    "the prefill (no packed copy on either path); global: "
+                    "keys read back from the pages just written"}
 
 
 def bench_adapters(tm, wl, steps, warmup, n_sets=2):
@@ -624,13 +627,22 @@ def bench_adapters(tm, wl, steps, warmup, n_sets=2):
                                  sets, max(5, steps // 5),
                                  max(2, warmup // 5))
         flops = 4 * D * HQ * wl.visible_pairs([T] * Bp, window or 0)
+        # the same call with token-major K/V ([B, HK, T, D] contiguous):
+        # the channel-major source against the row source, same kernel
+        tm_sets = [(a[0], a[1].contiguous(), a[2].contiguous()) + a[3:]
+                   for a in sets]
+        _, ms_tm = time_launches(lambda a: compat.attn_prefill_fused(*a),
+                                 tm_sets, max(5, steps // 5),
+                                 max(2, warmup // 5))
+        del tm_sets
         res[f"attn_prefill_fused_{kind}_b6_t1536"] = {
             "ms_per_call": ms, "flops_per_call": flops,
             "tflops": flops / (ms * 1e-3) / 1e12,
             "roofline_frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
             "reference_b300_ms": ref_ms[kind],
             "speedup_vs_reference_b300": ref_ms[kind] / ms,
-            "kv_layout": "channel-major (stride 1 along T)"}
+            "kv_layout": "channel-major (stride 1 along T), read in place",
+            "ms_per_call_token_major_kv": ms_tm}
         res[f"prefill_layer_{kind}_b6_t1536_with_append"] = \
             bench_prefill_append(tm, compat, sets, window, HKV, steps,
                                  warmup)

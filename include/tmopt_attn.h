@@ -283,14 +283,28 @@ int tmopt_attn_decode_paged_noalloc(const void* q, const void* k_pool,
  *         (prior_lens NULL = all zero).
  * Keys of sequence i are positions [0, prior_lens[i] + len_i). They come
  * from one of three sources:
- *   block_table == NULL (packed): k, v [total_q, HKV, D] (strides as q)
- *         hold the run's own keys; prior_lens and table_wrap must be 0.
+ *   block_table == NULL (packed): k, v hold the run's own keys; prior_lens
+ *         and table_wrap must be 0. Key j of run i, head h, dim d sits at
+ *         element base_i + j * k_stride_tok + h * k_stride_head +
+ *         d * k_stride_dim, where base_i = i * k_stride_run, or
+ *         cu_seqlens_q[i] * k_stride_tok when k_stride_run is 0 (likewise
+ *         v). Token-major rows: k_stride_dim == 1, k_stride_tok % 8 == 0.
+ *         Channel-major rows (tokens contiguous, head_dim strided: the
+ *         sconv output the reference hands to attn_prefill_fused,
+ *         attn_prefill.py:162-168, experiments/DEADENDS.md:631-645):
+ *         k_stride_tok == 1, k_stride_dim % 8 == 0 and >= max_seqlen_q,
+ *         k_stride_run > 0; read in place. A channel-major row is read in
+ *         16-byte pieces, so up to 7 elements past a run's last key (within
+ *         the row) are read as well: they must be finite (they get zero
+ *         weight). Run, head strides % 8 == 0 and 16-byte aligned k / v in
+ *         both layouts.
  *   block_table != NULL, k == v == NULL (paged): every key is read from
  *         the paged pools (k_pool, v_pool, [num_pages, page_size, HKV, D])
  *         through block_table [num_seqs, bt_stride]; the run's new keys
  *         must already be written (tmopt_kv_write_paged). table_wrap = 0.
  *   block_table != NULL, k, v given (mixed): keys before prior_lens[i]
- *         from the pools, the run's own keys from packed k / v. The run's
+ *         from the pools, the run's own keys from packed, token-major
+ *         k / v (addressed as above). The run's
  *         keys need not be in the pool yet: append them afterwards. With
  *         table_wrap > 0 each table row is a ring of table_wrap pages
  *         holding the last table_wrap * page_size positions (RingKV /
@@ -327,8 +341,10 @@ int tmopt_attn_decode_paged_noalloc(const void* q, const void* k_pool,
  */
 int tmopt_attn_prefill_varlen(
     const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k,
-    int64_t k_stride_tok, int64_t k_stride_head, const void* v,
-    int64_t v_stride_tok, int64_t v_stride_head, const int32_t* cu_seqlens_q,
+    int64_t k_stride_run, int64_t k_stride_tok, int64_t k_stride_head,
+    int64_t k_stride_dim, const void* v, int64_t v_stride_run,
+    int64_t v_stride_tok, int64_t v_stride_head, int64_t v_stride_dim,
+    const int32_t* cu_seqlens_q,
     const int32_t* prior_lens, int num_seqs, int max_seqlen_q,
     const void* k_pool, const void* v_pool, const int32_t* block_table,
     int64_t bt_stride, int table_wrap, int page_size, int64_t num_pages,

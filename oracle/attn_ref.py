@@ -182,20 +182,26 @@ def decode_reference_semantics(q, pool_k, pool_v, slots, pos, rel, window):
                         table_wrap=per, rel=rel)
 
 
-def prefill_reference_semantics(q, k, v, rel, positions, window):
+def prefill_reference_semantics(q, k, v, rel, positions, window,
+                                rows=None):
     """attn_prefill_fused's model semantics on the padded batch
     (engine/pyengine/kernels/attn_prefill.py:114-124, the eager chain
     model.py:530-556 with rel_bias model.py:137-158): score = q.k / D +
     rel[b, h, q, clamp(dist, 0, E-1)] zeroed outside 0 <= dist < E, kept
     iff 0 <= dist (< window on SWA layers), fp32 softmax.
     q [B, H, T, D], k/v [B, HK, T, D], rel [B, H, T, E], positions [T].
-    Returns [B, T, H, D] fp32."""
+    rows: optional query indices; only those query rows are computed (the
+    same expressions restricted to them, for shapes whose full [T, T]
+    scores would not fit).
+    Returns [B, T, H, D] fp32 ([B, len(rows), H, D] with rows)."""
     B, H, T, D = q.shape
     HK = k.shape[1]
     E = rel.shape[3]
     rep = H // HK
     pos = positions.to(torch.int64).cpu()
-    dist = pos[:, None] - pos[None, :]                       # [T, T]
+    qsel = torch.arange(T) if rows is None else torch.as_tensor(rows)
+    M = qsel.shape[0]
+    dist = pos[qsel, None] - pos[None, :]                    # [M, T]
     idx = dist.clamp(0, E - 1)
     band = (dist >= 0) & (dist < E)
     keep = dist >= 0
@@ -203,9 +209,10 @@ def prefill_reference_semantics(q, k, v, rel, positions, window):
         keep &= dist < window
     kh = k.float().repeat_interleave(rep, 1)
     vh = v.float().repeat_interleave(rep, 1)
-    s = torch.matmul(q.float(), kh.transpose(2, 3)) / D      # [B,H,T,T]
-    r = rel.float()
-    bias = torch.gather(r, 3, idx[None, None].expand(B, H, T, T))
+    qf = q[:, :, qsel].float()
+    s = torch.matmul(qf, kh.transpose(2, 3)) / D             # [B,H,M,T]
+    r = rel[:, :, qsel].float()
+    bias = torch.gather(r, 3, idx[None, None].expand(B, H, M, T))
     s = s + torch.where(band[None, None], bias, torch.zeros(()))
     s = s.masked_fill(~keep[None, None], -math.inf)
     p = torch.softmax(s, -1)

@@ -72,15 +72,16 @@ def test_invalid_arguments_return_status(tm):
         assert rc == tm._lib.TMOPT_EINVAL
         assert b"ring of 4 pages" in lib.tmopt_last_error()
     # prefill: REP 3 is unsupported
-    rc = lib.tmopt_attn_prefill_varlen(p, 0, 0, p, 0, 0, p, 0, 0, p, null, 1,
-                                       4, null, null, null, 0, 0, 16, 0, 12,
-                                       4, 128, 0, 0.1, null, 0, 0, 0, p, 0, 0,
-                                       null, null, null)
+    rc = lib.tmopt_attn_prefill_varlen(p, 0, 0, p, 0, 0, 0, 1, p, 0, 0, 0,
+                                       1, p, null, 1, 4, null, null, null, 0,
+                                       0, 16, 0, 12, 4, 128, 0, 0.1, null, 0,
+                                       0, 0, p, 0, 0, null, null, null)
     assert rc == tm._lib.TMOPT_EUNSUPPORTED
 
     def prefill(k, prior, table, wrap, window):
         return lib.tmopt_attn_prefill_varlen(
-            p, 4096, 128, k, 512, 128, k, 512, 128, p, prior, 1, 64, p, p,
+            p, 4096, 128, k, 0, 512, 128, 1, k, 0, 512, 128, 1, p, prior, 1,
+            64, p, p,
             table, 8, wrap, 16, 100, 32, 4, 128, window, 0.1, null, 0, 0, 0,
             p, 4096, 128, null, null, null)
     # prefill: a ring table needs the run's own k/v (mixed source) and a
@@ -89,11 +90,32 @@ def test_invalid_arguments_return_status(tm):
         assert prefill(k, p, p, 8, window) == tm._lib.TMOPT_EINVAL
         assert b"ring table" in lib.tmopt_last_error()
     rc = lib.tmopt_attn_prefill_varlen(
-        p, 4096, 128, p, 512, 128, p, 512, 128, p, p, 1, 64, null, null,
-        null, 0, 0, 16, 0, 32, 4, 128, 0, 0.1, null, 0, 0, 0, p, 4096, 128,
-        null, null, null)
+        p, 4096, 128, p, 0, 512, 128, 1, p, 0, 512, 128, 1, p, p, 1, 64, null,
+        null, null, 0, 0, 16, 0, 32, 4, 128, 0, 0.1, null, 0, 0, 0, p, 4096,
+        128, null, null, null)
     assert rc == tm._lib.TMOPT_EINVAL
     assert b"prior context needs a block table" in lib.tmopt_last_error()
+
+    # prefill, channel-major k/v (stride_tok 1, head_dim strided): they
+    # need a run stride, rows holding max_seqlen tokens, both tensors in
+    # the same layout, and the packed source
+    def prefill_cm(run, tok, dim, v_tok, v_dim, table=None):
+        return lib.tmopt_attn_prefill_varlen(
+            p, 4096, 128, p, run, tok, 128 * dim, dim, p, run, v_tok,
+            128 * v_dim, v_dim, p, null, 2, 64, p if table else null,
+            p if table else null, table, 8 if table else 0, 0, 16,
+            100 if table else 0, 32, 4, 128, 0, 0.1, null, 0, 0, 0, p, 4096,
+            128, null, null, null)
+    assert prefill_cm(0, 1, 64, 1, 64) == tm._lib.TMOPT_EINVAL
+    assert b"need a run stride" in lib.tmopt_last_error()
+    assert prefill_cm(4 * 128 * 64, 1, 64, 512, 1) == tm._lib.TMOPT_EINVAL
+    assert b"both channel-major" in lib.tmopt_last_error()
+    assert prefill_cm(4 * 128 * 56, 1, 56, 1, 56) == tm._lib.TMOPT_EINVAL
+    assert b"hold max_seqlen_q tokens" in lib.tmopt_last_error()
+    assert prefill_cm(4 * 128 * 68, 1, 68, 1, 68) == tm._lib.TMOPT_EINVAL
+    assert prefill_cm(4 * 128 * 64, 1, 64, 1, 64, table=p) == \
+        tm._lib.TMOPT_EUNSUPPORTED
+    assert b"only as the packed source" in lib.tmopt_last_error()
     # kv write: misaligned strides
     rc = lib.tmopt_kv_write_slots(p, p, 3, 8, 8, 8, p, 1, 4, 128, p, p, 10,
                                   null)
@@ -140,9 +162,9 @@ C_CALLER = r"""
 int main(void) {
   size_t ws = tmopt_attn_decode_workspace_size(64, 32, 4, 128, 0);
   int rc = tmopt_attn_prefill_varlen(
-      NULL, 0, 0, NULL, 0, 0, NULL, 0, 0, NULL, NULL, 1, 16, NULL, NULL,
-      NULL, 0, 0, 16, 0, 32, 4, 128, 0, 0.1f, NULL, 0, 0, 0, NULL, 0, 0,
-      NULL, NULL, NULL);
+      NULL, 0, 0, NULL, 0, 0, 0, 1, NULL, 0, 0, 0, 1, NULL, NULL, 1, 16,
+      NULL, NULL, NULL, 0, 0, 16, 0, 32, 4, 128, 0, 0.1f, NULL, 0, 0, 0,
+      NULL, 0, 0, NULL, NULL, NULL);
   printf("%s|%zu|%d|%s\n", tmopt_version(), ws, rc, tmopt_last_error());
   return rc == TMOPT_EINVAL && ws > 0 &&
          strstr(tmopt_last_error(), "null") != NULL ? 0 : 1;

@@ -77,8 +77,9 @@ def test_attn_global_flat_rows(tm, dev):
 @pytest.mark.parametrize("hq,hk", [(32, 4), (64, 16)])
 @pytest.mark.parametrize("T", [200, 77])
 def test_attn_prefill_fused_padded_batch(tm, dev, window, E, hq, hk, T):
-    """T = 200: the channel-major K/V are packed on chip (rows starting
-    mid-page: 200 % 16 = 8); T = 77 (not a multiple of 8): the copy path."""
+    """T = 200: the kernel reads the channel-major K/V in place (runs of
+    200 keys at the batch stride, last tile partial); T = 77 (not a
+    multiple of 8, so dim rows are not 16-byte aligned): the copy path."""
     g = torch.Generator().manual_seed(15)
     B, D = 3, 128
     q = torch.randn((B, T, hq, D), generator=g).to(torch.bfloat16).transpose(
@@ -145,20 +146,22 @@ def test_positions_check_lengths(tm, dev):
                 assert int(tm.prefill_check_positions(q, k)) == 1, (T, which)
 
 
+@pytest.mark.parametrize("T,lens", [(200, [200, 150, 77]), (77, [77, 60, 5])])
 @pytest.mark.parametrize("kind", ["global", "swa"])
-def test_attn_prefill_fused_populates_caches(tm, dev, kind):
+def test_attn_prefill_fused_populates_caches(tm, dev, kind, T, lens):
     """attn_prefill_fused given the rows' caches (the engine's
     st.cache.append(kn[i, :lens[i]], vv[i, :lens[i]]) at model.py:507-512)
     appends the channel-major K/V itself; a global layer then reads its keys
-    back from the pages (no packed copy), an SWA layer keeps the packed
-    source and fills its rings. The live rows equal the packed path's
-    bitwise, every cache holds its row's tokens bit-exact, n advances."""
+    back from the pages, an SWA layer reads the K/V tensors and fills its
+    rings. The live rows equal the cache-less path's bitwise, every cache
+    holds its row's tokens bit-exact, n advances. T = 77: channel-major dim
+    rows that are not 16-byte aligned, which neither kernel reads in place:
+    the adapter copies them before it touches any cache."""
     import numpy as np
     from helpers import PagedCache, RingCache
     from oracle import kv_ref
     g = torch.Generator().manual_seed(17)
-    B, T, D = 3, 200, 128
-    lens = [200, 150, 77]
+    B, D = 3, 128
     if kind == "global":
         hq, hk, E, window = 64, 8, 1024, None
     else:
@@ -224,3 +227,61 @@ def test_attn_swa_model_shape_ring_grid(tm, dev):
                       slots.to(dev), pos.to(dev), rel.to(dev))
     torch.cuda.synchronize()
     assert_out_close(out, ref, "attn_swa model shape")
+
+
+def _edge_rows(T, extra, g):
+    """Query rows for sampled checks: the run's ends, the band edges of
+    the model's extents (511-513, 1023-1025) and random ones."""
+    fixed = [0, 1, 2, 63, 64, 65, 255, 256, 511, 512, 513, 1023, 1024,
+             1025, T - 2, T - 1]
+    rnd = torch.randint(0, T, (extra,), generator=g).tolist()
+    return sorted({r for r in fixed + rnd if 0 <= r < T})
+
+
+@pytest.mark.parametrize("with_caches", [False, True])
+@pytest.mark.parametrize("kind", ["swa", "global"])
+def test_attn_prefill_fused_model_shape(tm, dev, kind, with_caches):
+    """attn_prefill_fused at the shape the bench's adapter lines time
+    (B = 6, T = 1536; SWA 64Q/16KV, W = E = 512; global 64Q/8KV, E =
+    1024), K/V channel-major as the sconv hands them over (read in place),
+    with and without the rows' caches (rings / shared page pool with a
+    shuffled free list), on sampled rows of every batch row against the
+    oracle's model semantics."""
+    from helpers import PagedCache, RingCache
+    g = torch.Generator().manual_seed(19)
+    gd = torch.Generator(device=dev).manual_seed(19)
+    B, T, D = 6, 1536, 128
+    if kind == "global":
+        hq, hk, E, window = 64, 8, 1024, None
+    else:
+        hq, hk, E, window = 64, 16, 512, 512
+    bf = torch.bfloat16
+
+    def rnd(*shape, s=1.0):
+        return (torch.randn(shape, generator=gd, device=dev) * s).to(bf)
+    q = rnd(B, T, hq, D).transpose(1, 2)                       # [B,H,T,D]
+    k = rnd(B, hk * D, T).transpose(1, 2).view(B, T, hk, D).transpose(1, 2)
+    v = rnd(B, hk * D, T).transpose(1, 2).view(B, T, hk, D).transpose(1, 2)
+    assert k.stride(2) == 1 and k.stride(3) == T            # channel-major
+    rel = rnd(B, T, hq, E, s=0.5).transpose(1, 2)              # [B,H,T,E]
+    ar = torch.arange(T, device=dev)
+    caches = None
+    if with_caches and kind == "global":
+        P = B * T // 16 + 64
+        free = torch.randperm(P, generator=g).tolist()
+        kp = torch.zeros((P, 16, hk, D), dtype=bf, device=dev)
+        vp = torch.zeros_like(kp)
+        caches = [PagedCache(kp, vp, free, torch.zeros(
+            T // 16 + 8, dtype=torch.int64, device=dev)) for _ in range(B)]
+    elif with_caches:
+        caches = [RingCache(torch.zeros((E, hk, D), dtype=bf, device=dev),
+                            torch.zeros((E, hk, D), dtype=bf, device=dev))
+                  for _ in range(B)]
+    out = tm.attn_prefill_fused(q, k, v, rel, ar, ar, window, caches=caches)
+    torch.cuda.synchronize()
+    assert out.shape == (B, T, hq, D)
+    rows = _edge_rows(T, 24, g)
+    ref = attn_ref.prefill_reference_semantics(
+        q.cpu(), k.cpu(), v.cpu(), rel.cpu(), ar.cpu(), window, rows=rows)
+    assert_out_close(out[:, rows], ref,
+                     f"prefill_fused {kind} B6 T1536 caches={with_caches}")

@@ -96,10 +96,9 @@ def test_decode_step_graph_replays(tm, dev):
 
 def test_prefill_fused_first_call_in_capture(tm, dev):
     """attn_prefill_fused with channel-major K/V and the fused bias,
-    captured in a hipGraph on its first call for the shape (the on-chip
-    packing's identity table and the position check are then built inside
-    the capture): every replay, with eager work and a synchronisation
-    between replays, equals the eager call bitwise."""
+    captured in a hipGraph (its run offsets and the position check are then
+    built inside the capture): every replay, with eager work and a
+    synchronisation between replays, equals the eager call bitwise."""
     compat = import_module("tm-opt_amd.compat")
     g = torch.Generator().manual_seed(23)
     B, T, D, hq, hk, W = 2, 136, 128, 32, 4, 64
@@ -113,7 +112,6 @@ def test_prefill_fused_first_call_in_capture(tm, dev):
             torch.arange(T, device=dev), W)
     eager = tm.attn_prefill_fused(*args)
     torch.cuda.synchronize()
-    compat._PACK_META.clear()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         out = tm.attn_prefill_fused(*args)

@@ -1,25 +1,62 @@
-"""CPU checks of the package's host-side logic (no GPU): the table math
-the adapters hand to the kernels."""
+"""CPU checks of the package's host-side logic (no GPU): the layouts the
+adapters hand to the kernels."""
 from importlib import import_module
 
 import pytest
 import torch
 
 
-@pytest.mark.parametrize("B,T", [(1, 8), (3, 200), (6, 1536), (5, 24), (2, 16)])
-def test_pack_meta_is_an_identity_layout(B, T):
-    """The identity tables that pack channel-major K/V through the paged
-    write (compat._pack_meta): under the page rule, position start + i of
-    row b is packed row b*T + i for every i < T, and no table entry read for
-    those positions leaves the buffer."""
+def _cm(B, HK, T, D=128):
+    """[B, HK, T, D] K/V in the sconv's channel-major layout: the view of a
+    [B, HK*D, T] tensor (stride 1 along T, stride T along head_dim)."""
+    x = torch.zeros((B, HK * D, T), dtype=torch.bfloat16)
+    return x.transpose(1, 2).view(B, T, HK, D).transpose(1, 2)
+
+
+@pytest.mark.parametrize("B,T", [(1, 8), (3, 200), (6, 1536), (2, 16)])
+def test_kv_rows_reads_channel_major_in_place(B, T):
+    """compat._kv_rows hands channel-major K/V with 16-byte aligned dim rows
+    (T % 8 == 0) to the kernels as a view of the same memory: run stride =
+    batch stride, token stride 1, dim stride T (what the prefill's
+    channel-major source and the KV write read in place)."""
     compat = import_module("tm-opt_amd.compat")
-    start, lens, table = compat._pack_meta(B, T, "cpu")
-    P = (B * T + 15) // 16
-    assert table.is_contiguous() and table.shape[0] == B
-    assert torch.equal(lens, torch.full((B,), T, dtype=torch.int32))
-    for b in range(B):
-        pos = int(start[b]) + torch.arange(T)
-        assert int(pos[-1]) // 16 < table.shape[1]
-        rows = table[b][pos // 16].long() * 16 + pos % 16
-        assert torch.equal(rows, b * T + torch.arange(T))
-        assert int(table[b][pos // 16].max()) < P
+    HK, D = 4, 128
+    k = _cm(B, HK, T, D)
+    r = compat._kv_rows(k)
+    assert r.shape == (B, T, HK, D)
+    assert r.data_ptr() == k.data_ptr()
+    assert r.stride()[1:] == (1, D * T, T)
+    assert r.stride(0) % 8 == 0 and (B == 1 or r.stride(0) == HK * D * T)
+    assert torch.equal(r, k.transpose(1, 2))
+
+
+@pytest.mark.parametrize("B,T", [(3, 77), (1, 5), (2, 100)])
+def test_kv_rows_copies_unaligned_channel_major(B, T):
+    """Channel-major rows whose dim stride is not a multiple of 8 (T % 8 !=
+    0) are read by neither kernel: a token-major copy with the same
+    values (the adapter makes it before it touches any cache)."""
+    compat = import_module("tm-opt_amd.compat")
+    g = torch.Generator().manual_seed(B * 1000 + T)
+    HK, D = 2, 128
+    x = torch.randn((B, HK * D, T), generator=g).to(torch.bfloat16)
+    k = x.transpose(1, 2).view(B, T, HK, D).transpose(1, 2)
+    r = compat._kv_rows(k)
+    assert r.data_ptr() != k.data_ptr() and r.is_contiguous()
+    assert torch.equal(r, k.transpose(1, 2))
+
+
+def test_kv_rows_token_major_views():
+    """Token-major K/V (a [B, HK, T, D] view of [B, T, HK, D] rows, or a
+    contiguous [B, HK, T, D]) are read in place; a size-1 batch axis with an
+    odd stride is fixed up without a copy."""
+    compat = import_module("tm-opt_amd.compat")
+    B, HK, T, D = 3, 4, 37, 128
+    a = torch.zeros((B, T, HK, D), dtype=torch.bfloat16).transpose(1, 2)
+    b = torch.zeros((B, HK, T, D), dtype=torch.bfloat16)
+    for x in (a, b):
+        r = compat._kv_rows(x)
+        assert r.data_ptr() == x.data_ptr() and r.stride(3) == 1
+    one = torch.zeros((HK * D * 8 + 4,), dtype=torch.bfloat16)[:HK * D * 8]
+    one = one.as_strided((1, HK, 8, D), (3, D * 8, 1, 8))
+    r = compat._kv_rows(one)
+    assert r.data_ptr() == one.data_ptr() and r.stride(0) % 8 == 0

@@ -395,6 +395,12 @@ def test_varlen_bias_matches_padded_semantics():
         b, _ = attn_ref.prefill_varlen(pk(q), pk(k), pk(v), cu, 1.0 / D,
                                        window=window or 0, rel=pk(rel))
         assert (a.reshape(B * T, H, D) - b).abs().max() < 1e-5, window
+        # sampled query rows (the form the model-shape GPU tests use) are
+        # the same rows of the whole-batch result
+        rows = [44, 0, 10, 11, 29]
+        sub = attn_ref.prefill_reference_semantics(
+            q, k, v, rel, torch.arange(T), window, rows=rows)
+        assert (sub - a[:, rows]).abs().max() < 1e-5, window
 
 
 # --------------------------------------------------------------------------

@@ -69,8 +69,9 @@ SIGNATURES = {
         _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_f32, _c_ptr,
         _c_i32, _c_i32, _c_i32, _c_ptr, _c_ptr, _c_ptr]),
     "tmopt_attn_prefill_varlen": (_c_i32, [
-        _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64,
-        _c_i64, _c_ptr, _c_ptr, _c_i32, _c_i32, _c_ptr, _c_ptr, _c_ptr,
+        _c_ptr, _c_i64, _c_i64, _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64,
+        _c_ptr, _c_i64, _c_i64, _c_i64, _c_i64,
+        _c_ptr, _c_ptr, _c_i32, _c_i32, _c_ptr, _c_ptr, _c_ptr,
         _c_i64, _c_i32, _c_i32, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,
         _c_f32, _c_ptr, _c_i64, _c_i64, _c_i32,
         _c_ptr, _c_i64, _c_i64, _c_ptr, _c_ptr, _c_ptr]),

@@ -324,8 +324,13 @@ def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, max_seqlen=None,
     q [total, HQ, D] bf16 (D contiguous, any token / head strides);
     cu_seqlens [S+1] int32. Query j of run i sits at position
     prior_lens[i] + j. Key sources:
-      * block_table None: k/v [total, HKV, D] hold each run's own keys
-        (no prior context);
+      * block_table None: k/v hold each run's own keys (no prior context):
+        [total, HKV, D] packed like q, or [S, T, HKV, D] with run i's keys
+        in its first len_i rows (a padded batch read in place, T >=
+        max_seqlen). Either token-major (head_dim contiguous) or
+        channel-major (tokens contiguous, head_dim strided: the sconv
+        output, attn_prefill.py:162-168), the latter in the [S, T, HKV, D]
+        form only, T % 8 == 0;
       * block_table given, k/v None: every key, prior context included, is
         read from k_pool/v_pool [num_pages, 16, HKV, D] through block_table
         (int32 [S, bt_stride]); the run's own keys must already be there;
@@ -369,17 +374,31 @@ def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, max_seqlen=None,
         assert own, "the packed source needs k and v"
         assert not table_wrap
         P, page_size = 0, PAGE_SIZE
-    ks = vs = (0, 0)
+    ks = vs = (0, 0, 0, 1)
     if own:
         assert k is not None and v is not None
-        _check_rows(k, "k")
-        _check_rows(v, "v")
-        assert k.shape[0] == total and v.shape == k.shape and k.shape[2] == D
+        assert v.shape == k.shape and k.shape[-1] == D
+        for x, name in ((k, "k"), (v, "v")):
+            assert x.dtype == torch.bfloat16, f"{name} must be bf16"
+        if k.dim() == 3:                       # packed by cu_seqlens
+            _check_rows(k, "k")
+            _check_rows(v, "v")
+            assert k.shape[0] == total
+            ks = (0, k.stride(0), k.stride(1), 1)
+            vs = (0, v.stride(0), v.stride(1), 1)
+        else:                                  # one padded row per run
+            assert k.dim() == 4 and k.shape[0] >= S
+            assert k.shape[1] >= max_seqlen, (k.shape, max_seqlen)
+            for x, name in ((k, "k"), (v, "v")):
+                assert x.stride(3) == 1 or x.stride(1) == 1, \
+                    f"{name}: head_dim or tokens must be contiguous"
+            ks = (k.stride(0), k.stride(1), k.stride(2), k.stride(3))
+            vs = (v.stride(0), v.stride(1), v.stride(2), v.stride(3))
         if pooled:
-            assert k.shape[1] == HKV
-        HKV = k.shape[1]
-        ks = (k.stride(0), k.stride(1))
-        vs = (v.stride(0), v.stride(1))
+            assert k.shape[-2] == HKV
+            assert ks[3] == 1 and vs[3] == 1, \
+                "the mixed source reads token-major k/v"
+        HKV = k.shape[-2]
     assert HQ % HKV == 0
     if rel is not None:
         assert rel.dtype == torch.bfloat16 and rel.stride(2) == 1
@@ -392,8 +411,8 @@ def prefill_varlen(q, k, v, cu_seqlens, scale, window=0, max_seqlen=None,
     if lse is None and return_lse:
         lse = torch.empty((HQ, total), dtype=torch.float32, device=dev)
     _lib.call("tmopt_attn_prefill_varlen", _ptr(q), q.stride(0), q.stride(1),
-              _ptr(k) if own else None, ks[0], ks[1],
-              _ptr(v) if own else None, vs[0], vs[1], _ptr(cu_seqlens),
+              _ptr(k) if own else None, *ks,
+              _ptr(v) if own else None, *vs, _ptr(cu_seqlens),
               _ptr(prior_lens), S, int(max_seqlen),
               _ptr(k_pool) if pooled else None,
               _ptr(v_pool) if pooled else None, _ptr(block_table),

@@ -13,16 +13,17 @@ output layouts, and run the gfx950 kernels of this package:
   * the global path's per-token flat rows `flat` [B, Lg] (model.py:938-945)
     are turned back into a block table: rows of one page are consecutive,
     so page i of row b is flat[b, 16 i] // 16;
-  * the padded [B, H, T, D] prefill batch becomes B packed runs of T tokens
-    (cu_seqlens = 0, T, 2T, ...), read in place when the strides allow;
-    channel-major K/V (the sconv output) are packed on chip by the paged
-    write's transposing kernel, other layouts copied;
+  * the padded [B, H, T, D] prefill batch becomes B runs of T tokens
+    (cu_seqlens = 0, T, 2T, ...): queries as packed rows, K/V one run per
+    batch row at the batch stride, token-major or channel-major (the sconv
+    output) read in place, other layouts copied;
   * the prefill's position contract is checked on the device
     (tmopt_prefill_check_positions feeds the kernel's reject flag).
 
 No host synchronisation in attn_swa, attn_global, attn_prefill_fused
-without caches and the pooled chunk adapters: every helper tensor is built
-with device ops, so they can run inside hipGraph capture. The
+without caches and the pooled chunk adapters given max_seqlen (or one
+sequence, cu_seqlens None): every helper tensor is built with device ops,
+so they can run inside hipGraph capture. The
 cache-populating paths take the rows' lengths from the host cache
 objects, as the reference's appends do (their small metadata tensors go
 through pinned memory, without a stream synchronisation).
@@ -99,55 +100,28 @@ def _packed(x, B, T, H, D):
     return xt.as_strided((B * T, H, D), (xt.stride(1), xt.stride(2), 1))
 
 
-# per (B, T, device): the identity page tables of _pack_channel_major, built
-# once per shape; the oldest entries go first past _PACK_META_MAX shapes
-_PACK_META = {}
-_PACK_META_MAX = 64
-
-
-def _pack_meta(B, T, dev):
-    """Identity tables of a [B*T]-row packed buffer seen as 16-row pages:
-    (start [B], lens [B], table [B, w]) int32, so that position start[b] + i
-    of row b lands in packed row b*T + i under the page rule
-    table[p // 16] * 16 + p % 16 (entries past the buffer clamp to its last
-    page and are never reached). Built with device ops: no host copy, so it
-    is also legal inside a graph capture."""
-    P = (B * T + PAGE - 1) // PAGE
-    w = (T + PAGE - 1) // PAGE + 1
-    start = torch.arange(B, dtype=torch.int32, device=dev) * T
-    table = torch.clamp(
-        torch.arange(w, dtype=torch.int32, device=dev)[None] +
-        (start // PAGE)[:, None], max=P - 1).contiguous()
-    lens = torch.full((B,), T, dtype=torch.int32, device=dev)
-    return start % PAGE, lens, table
-
-
-def _pack_channel_major(k, v, B, T, H, D):
-    """Channel-major [B, H, T, D] K/V views (the sconv output: tokens
-    contiguous) -> packed [B*T, H, D] rows, transposed on chip by one
-    batched append over identity tables: the packed buffer is a pool of
-    16-row pages, row b starts at page (b*T)//16, slot (b*T)%16. None when
-    the layout is outside what that kernel reads (then the caller copies)."""
-    kt, vt = k.transpose(1, 2), v.transpose(1, 2)       # [B, T, H, D]
-    if not (T % 8 == 0 and D == attn.HEAD_DIM and
-            all(x.stride(1) == 1 and x.stride(3) != 1 and
-                x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
-                for x in (kt, vt))):
-        return None
-    dev = k.device
-    P = (B * T + PAGE - 1) // PAGE
-    key = (B, T, dev)
-    meta = _PACK_META.get(key)
-    if meta is None:
-        meta = _pack_meta(B, T, dev)
-        if len(_PACK_META) >= _PACK_META_MAX:
-            _PACK_META.pop(next(iter(_PACK_META)))
-        _PACK_META[key] = meta
-    start, lens, table = meta
-    kp = torch.empty((P, PAGE, H, D), dtype=k.dtype, device=dev)
-    vp = torch.empty_like(kp)
-    attn.kv_append_rows(kt, vt, lens, start, table, kp, vp, max_len=T)
-    return (kp.view(P * PAGE, H, D)[:B * T], vp.view(P * PAGE, H, D)[:B * T])
+def _kv_rows(x):
+    """[B, HK, T, D] K or V (any strides) -> a [B, T, HK, D] view that the
+    prefill and the KV write both read in place: token-major rows (head_dim
+    contiguous) or channel-major ones (tokens contiguous, head_dim strided:
+    the sconv output, experiments/DEADENDS.md:631-645), with 16-byte
+    aligned rows, dim rows and heads. Anything else (e.g. channel-major with
+    T % 8 != 0) becomes a token-major copy, so a caller can rely on both
+    kernels accepting the result before it changes any cache."""
+    xt = x.transpose(1, 2)                       # [B, T, HK, D]
+    B, T, _, D = xt.shape
+    if B == 1 and xt.stride(0) % 8 != 0:
+        # a size-1 axis: its stride never moves an address
+        xt = xt.as_strided(xt.shape, (8,) + tuple(xt.stride()[1:]))
+    st = xt.stride()
+    aligned = (xt.data_ptr() % 16 == 0 and st[0] % 8 == 0 and
+               st[2] % 8 == 0)
+    token_major = st[3] == 1 and st[1] % 8 == 0
+    channel_major = (st[1] == 1 and D == attn.HEAD_DIM and st[3] % 8 == 0 and
+                     st[3] >= T)
+    if aligned and (token_major or channel_major):
+        return xt
+    return xt.contiguous()
 
 
 def _to_device(rows, dev):
@@ -164,7 +138,9 @@ def _append_rows(k, v, caches, lens):
     """The prefill's cache population (model.py:507-512:
     st.cache.append(kn[i, :lens[i]], vv[i, :lens[i]])) done natively: each
     row's K/V [lens[i], HK, D] is appended to its cache straight from the
-    (channel-major or token-major) views, pages allocated on the host as
+    [B, T, HK, D] rows of _kv_rows (channel-major or token-major, a layout
+    the write kernels accept, checked before any cache changes), pages
+    allocated on the host as
     PagedKV.append does (kv.py:196-198), ring rows as RingKV.append keeps
     them (kv.py:89-103); cache.n advances. Page caches that share one pool
     (GlobalPool rows) take one batched launch for all rows; rings and
@@ -199,12 +175,12 @@ def _append_rows(k, v, caches, lens):
                            for c in caches)
     if shared:
         c0 = caches[0]
-        attn.kv_append_rows(k.transpose(1, 2), v.transpose(1, 2), lens_d,
-                            start, rows, c0.kp, c0.vp, max_len=max(T))
+        attn.kv_append_rows(k, v, lens_d, start, rows, c0.kp, c0.vp,
+                            max_len=max(T))
     else:
         for i, c in enumerate(caches):
-            kt = k[i].transpose(0, 1)[:T[i]]     # [T, HK, D] view
-            vt = v[i].transpose(0, 1)[:T[i]]
+            kt = k[i, :T[i]]                     # [T, HK, D] view
+            vt = v[i, :T[i]]
             cu = meta[2 * B + 2 * i:2 * B + 2 * i + 2]
             if hasattr(c, "kp"):
                 row = (rows[i:i + 1].contiguous() if rows is not None else
@@ -236,14 +212,18 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
     Returns [B, T, H, D] bf16. block_m / block_n are accepted for signature
     compatibility; the kernel's tiles are fixed for gfx950.
 
+    K/V are read in place in the layout they arrive in: the sconv's
+    channel-major output (stride 1 along T, attn_prefill.py:162-168) or
+    token-major rows; only layouts neither kernel reads (channel-major with
+    T % 8 != 0, misaligned views) are copied first.
+
     caches / lens (optional, not in the reference signature): the B rows'
     cache objects (PagedKV- or RingKV-shaped, empty: a whole-prompt
     prefill) and live lengths (default T) whose population the engine does
     just before this call (model.py:507-512). The adapter then appends the
-    rows itself, reading the sconv's channel-major K/V in place, and a
-    global layer's attention reads its keys back from those pages: the
-    packed copy of K/V is gone. Rings (SWA) cannot hold a prompt longer
-    than the window, so their attention keeps the packed source."""
+    rows itself from the same in-place K/V, and a global layer's attention
+    reads its keys back from those pages. Rings (SWA) cannot hold a prompt
+    longer than the window, so their attention reads the K/V tensors."""
     B, H, T, D = q.shape
     HK = k.shape[1]
     E = rel.shape[3]
@@ -281,13 +261,14 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
     out = torch.empty((B, T, H, D), dtype=q.dtype, device=dev)
     cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=dev)
     w = 0 if window is None else int(window)
+    kr, vr = _kv_rows(k), _kv_rows(v)            # [B, T, HK, D]
     table = None
     if caches is not None:
         assert len(caches) == B
         assert all(int(c.n) == 0 for c in caches), \
             "caches must be empty (chunked prefill: prefill_chunk_state)"
         lens = [T] * B if lens is None else [int(x) for x in lens]
-        table = _append_rows(k, v, caches, lens)
+        table = _append_rows(kr, vr, caches, lens)
         if not (table is not None and window is None and
                 all(c.kp is caches[0].kp for c in caches)):
             table = None
@@ -300,10 +281,7 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
                             out=out.view(B * T, H, D), return_lse=False,
                             reject=reject)
         return out
-    kv = _pack_channel_major(k, v, B, T, HK, D)
-    kp, vp = kv if kv is not None else (_packed(k, B, T, HK, D),
-                                        _packed(v, B, T, HK, D))
-    attn.prefill_varlen(qp, kp, vp, cu, 1.0 / D, window=w, max_seqlen=T,
+    attn.prefill_varlen(qp, kr, vr, cu, 1.0 / D, window=w, max_seqlen=T,
                         rel=relp, out=out.view(B * T, H, D),
                         return_lse=False, reject=reject)
     return out
@@ -323,14 +301,20 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
 # after the attention, which a ring requires (it overwrites positions the
 # chunk's first queries still see).
 
-def _chunk_cu(q, cu_seqlens):
+def _chunk_cu(q, cu_seqlens, max_seqlen):
+    """(cu_seqlens, max_seqlen) of a chunk batch: one sequence of
+    q.shape[0] tokens when cu_seqlens is None (no device read); otherwise
+    max_seqlen as given, or read back once (a host synchronisation, which a
+    graph capture must avoid by passing it) for both launches."""
     if cu_seqlens is None:
         cu = torch.full((2,), q.shape[0], dtype=torch.int32,
                         device=q.device)
         cu[0] = 0
-        return cu
+        return cu, q.shape[0]
     assert cu_seqlens.dtype == torch.int32
-    return cu_seqlens
+    if max_seqlen is None:
+        max_seqlen = int((cu_seqlens[1:] - cu_seqlens[:-1]).max())
+    return cu_seqlens, max_seqlen
 
 
 def attn_prefill_chunk_swa(q, k, v, rel, pool_k, pool_v, slots, prior,
@@ -343,6 +327,8 @@ def attn_prefill_chunk_swa(q, k, v, rel, pool_k, pool_v, slots, prior,
     extent = W as attn_swa asserts); slots [B] i64 ring rows; prior [B]
     i64 tokens each ring has seen (RingKV.n). Scale 1/D. Attends, then
     appends the chunks to the rings (only the last W positions survive).
+    max_seqlen: the longest chunk; with several sequences pass it to keep
+    the call free of host synchronisation (graph capture).
     Returns out [total, H, D] bf16."""
     total, H, D = q.shape
     S1, W, HK, _ = pool_k.shape
@@ -351,7 +337,7 @@ def attn_prefill_chunk_swa(q, k, v, rel, pool_k, pool_v, slots, prior,
     assert slots.dtype == torch.int64 and prior.dtype == torch.int64
     if rel is not None:
         assert rel.shape == (total, H, W), (rel.shape, (total, H, W))
-    cu = _chunk_cu(q, cu_seqlens)
+    cu, max_seqlen = _chunk_cu(q, cu_seqlens, max_seqlen)
     per = W // PAGE
     kp = pool_k.view(S1 * per, PAGE, HK, D)
     vp = pool_v.view(S1 * per, PAGE, HK, D)
@@ -378,7 +364,9 @@ def attn_prefill_chunk_global(q, k, v, rel, pool_kp, pool_vp, table_dev,
     (GlobalPool's device page table, already covering each sequence's
     prior + chunk positions: PagedKV.ensure_pages, kv.py:170-191); slots
     [B] i64; prior [B] i64 (PagedKV.n). Scale 1/D, causal. Attends, then
-    appends the chunks through the page table. Returns out [total, H, D]."""
+    appends the chunks through the page table. max_seqlen: the longest
+    chunk; with several sequences pass it to keep the call free of host
+    synchronisation (graph capture). Returns out [total, H, D]."""
     total, H, D = q.shape
     assert pool_kp.is_contiguous() and pool_vp.is_contiguous()
     assert pool_kp.shape[1] == PAGE
@@ -386,7 +374,7 @@ def attn_prefill_chunk_global(q, k, v, rel, pool_kp, pool_vp, table_dev,
     assert slots.dtype == torch.int64 and prior.dtype == torch.int64
     if rel is not None:
         assert rel.shape[:2] == (total, H)
-    cu = _chunk_cu(q, cu_seqlens)
+    cu, max_seqlen = _chunk_cu(q, cu_seqlens, max_seqlen)
     table = table_dev[slots].to(torch.int32)
     start = prior.to(torch.int32)
     out, _ = attn.prefill_varlen(q, k, v, cu, 1.0 / D, window=0,

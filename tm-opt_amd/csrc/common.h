@@ -106,6 +106,9 @@ typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
 __device__ __forceinline__ void lds_st64(uint32_t addr, u32x2 v) {
   *(lds_u32x2*)(uintptr_t)addr = v;
 }
+__device__ __forceinline__ u32x2 lds_ld64(uint32_t addr) {
+  return *(const lds_u32x2*)(uintptr_t)addr;
+}
 
 // ds_read_b64_tr_b16: within each 16-lane group, lane i receives element
 // i % 4 of the 8-byte chunks addressed by lanes 4j + i / 4 (j = 0..3), i.e.

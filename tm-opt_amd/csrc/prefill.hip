@@ -59,6 +59,9 @@ constexpr int kNStage = 4;                // 128 KB of LDS per work-group
 constexpr int kPage = 16;                 // paged source: tokens per page
 constexpr float kLazy = 8.0f;             // lazy-rescale threshold (log2)
 constexpr int kRing = 4;                  // MFMA-phase fragment ring
+// a buffer offset past every resource this kernel builds (their ranges are
+// checked below 2^31 - 16 on the host): the load returns zeros
+constexpr int kOob = 0x7ffffff0;
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
@@ -131,6 +134,8 @@ struct PrefillArgs {
   int64_t k_st, k_sh;
   const __bf16* v;
   int64_t v_st, v_sh;
+  int64_t k_sd, v_sd;   // head_dim strides (1: token-major rows)
+  int64_t k_sr, v_sr;   // run strides (0: run s starts at row cu[s])
   const int32_t* cu;
   const int32_t* prior;
   const __bf16* kpool;
@@ -269,11 +274,27 @@ enum Source : int {
   kPaged = 1,   // every key, prior and own, from the page pools
   kMixed = 2,   // keys before prior_lens[i] from the pools (or a ring of
                 // pages), the run's own keys from packed k / v
+  kPackedCM = 3,  // kPacked with channel-major k / v: tokens contiguous,
+                  // head_dim strided (the sconv output), read in place
 };
+
+// Channel-major tiles in LDS are 128 dim rows of 64 keys (128 bytes, eight
+// 16-byte chunks of 8 keys). Row r keeps logical chunk c in physical slot
+// c ^ cm_sig(r). cm_sig is a bijection of (r >> 1) & 7 that flips bit 2
+// between rows 4m and 4m + 2, so that
+//  * 16 consecutive rows reading one chunk (V^T fragments: a 16-lane group)
+//    hit 16 distinct 16-byte bank groups (8 slots x row parity), and
+//  * 4 consecutive rows reading an aligned group of 4 chunks (K fragments
+//    by transposed reads: a half wave) hit 16 distinct ones as well.
+__device__ __forceinline__ int cm_sig(int r) {
+  const int x = (r >> 1) & 7;
+  return ((x & 1) << 2) | (x >> 1);
+}
 
 template <int REP, bool REL, int SRC>
 __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
-  constexpr bool POOL = SRC != kPacked;   // some keys come from the pools
+  constexpr bool CM = SRC == kPackedCM;   // channel-major k / v tiles
+  constexpr bool POOL = SRC == kPaged || SRC == kMixed;  // keys from pools
   constexpr bool OWN = SRC != kPaged;     // the run's keys from packed k/v
   constexpr int BQ = 256 / REP;   // queries per work-group
   constexpr int QSUB = BQ / 32;   // 32-query sub-blocks per head
@@ -334,15 +355,42 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   constexpr bool VIS = REL;   // DMA the compiler can see (see dma())
   auto rk = mk_rsrc<VIS>(nullptr, 0u), rv = mk_rsrc<VIS>(nullptr, 0u);
   int kst_b = 0, vst_b = 0, klane_p = 0, vlane_p = 0;
+  [[maybe_unused]] int cm_key = 0;
   if constexpr (OWN) {
-    kst_b = (int)(a.k_st * 2);
-    vst_b = (int)(a.v_st * 2);
-    rk = mk_rsrc<VIS>(a.k + (int64_t)t0 * a.k_st + (int64_t)kvh * a.k_sh,
-                      (uint32_t)(((int64_t)(len - 1) * a.k_st + kD) * 2));
-    rv = mk_rsrc<VIS>(a.v + (int64_t)t0 * a.v_st + (int64_t)kvh * a.v_sh,
-                      (uint32_t)(((int64_t)(len - 1) * a.v_st + kD) * 2));
-    klane_p = grp * kst_b + 16 * kchunk;
-    vlane_p = grp * vst_b + 16 * vchunk;
+    // the run's first row: at row cu[s] of the packed rows, or at s times
+    // the run stride (a padded batch read in place)
+    const int64_t k0 = a.k_sr != 0 ? (int64_t)seq * a.k_sr
+                                   : (int64_t)t0 * a.k_st;
+    const int64_t v0 = a.v_sr != 0 ? (int64_t)seq * a.v_sr
+                                   : (int64_t)t0 * a.v_st;
+    if constexpr (CM) {
+      // 128 dim rows of the run's keys, a.k_sd elements apart: wave w
+      // moves dim rows 8w..8w+7 and 64+8w..64+8w+7 of the K and the V
+      // tile, lane l row l >> 3, physical slot l & 7, i.e. logical chunk
+      // (l & 7) ^ cm_sig(row) (the same for both blocks: their rows differ
+      // by 64). Chunks starting at or past the run end take an offset
+      // outside the resource and arrive as zeros.
+      kst_b = (int)(a.k_sd * 2);
+      vst_b = (int)(a.v_sd * 2);
+      rk = mk_rsrc<VIS>(a.k + k0 + (int64_t)kvh * a.k_sh,
+                        (uint32_t)(((int64_t)(kD - 1) * a.k_sd + len) * 2));
+      rv = mk_rsrc<VIS>(a.v + v0 + (int64_t)kvh * a.v_sh,
+                        (uint32_t)(((int64_t)(kD - 1) * a.v_sd + len) * 2));
+      const int r = 8 * w + (lane >> 3);
+      const int c = (lane & 7) ^ cm_sig(r);
+      cm_key = 8 * c;
+      klane_p = r * kst_b + 2 * cm_key;
+      vlane_p = r * vst_b + 2 * cm_key;
+    } else {
+      kst_b = (int)(a.k_st * 2);
+      vst_b = (int)(a.v_st * 2);
+      rk = mk_rsrc<VIS>(a.k + k0 + (int64_t)kvh * a.k_sh,
+                        (uint32_t)(((int64_t)(len - 1) * a.k_st + kD) * 2));
+      rv = mk_rsrc<VIS>(a.v + v0 + (int64_t)kvh * a.v_sh,
+                        (uint32_t)(((int64_t)(len - 1) * a.v_st + kD) * 2));
+      klane_p = grp * kst_b + 16 * kchunk;
+      vlane_p = grp * vst_b + 16 * vchunk;
+    }
   }
   // pool rows: keys below `plim` (all keys on the paged source, the prior
   // context on the mixed one)
@@ -399,24 +447,35 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   auto issue_tile = [&](int t, int st) {
     const int kt = k_lo + t * kBN;
     const uint32_t sb = lds0 + st * kStage;
+    if constexpr (CM) {
+      // dim rows 8w.. and 64+8w.. of the channel-major tile (see above)
+      const bool in = kt + cm_key < len;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int r0 = 4 * w + 32 * i;          // first row of the block
-      const uint32_t dk = sb + r0 * kRowB, dv = dk + kTileB;
-      const int key0 = kt + r0;
-      if constexpr (SRC == kPacked) {
-        own_dma(key0, dk, dv);
-      } else if constexpr (SRC == kPaged) {
-        pool_dma(key0, dk, dv);
-      } else {
-        if (key0 + 4 <= plim) {
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t dk = sb + (w + 8 * i) * 1024, dv = dk + kTileB;
+        dma(rk, dk, in ? klane_p + 64 * i * kst_b + 2 * kt : kOob);
+        dma(rv, dv, in ? vlane_p + 64 * i * vst_b + 2 * kt : kOob);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int r0 = 4 * w + 32 * i;          // first row of the block
+        const uint32_t dk = sb + r0 * kRowB, dv = dk + kTileB;
+        const int key0 = kt + r0;
+        if constexpr (SRC == kPacked) {
+          own_dma(key0, dk, dv);
+        } else if constexpr (SRC == kPaged) {
           pool_dma(key0, dk, dv);
-        } else if (key0 >= plim) {
-          own_dma(key0 - plim, dk, dv);
         } else {
-          // lane group grp holds row key0 + grp
-          if (key0 + grp < plim) pool_dma(key0, dk, dv);
-          else own_dma(key0 - plim, dk, dv);
+          if (key0 + 4 <= plim) {
+            pool_dma(key0, dk, dv);
+          } else if (key0 >= plim) {
+            own_dma(key0 - plim, dk, dv);
+          } else {
+            // lane group grp holds row key0 + grp
+            if (key0 + grp < plim) pool_dma(key0, dk, dv);
+            else own_dma(key0 - plim, dk, dv);
+          }
         }
       }
     }
@@ -437,27 +496,73 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
                                   64 * (s16 >> 2) + 32 * ((lane >> 4) & 1) +
                                   8 * (s16 & 3));
 
+  // Channel-major tiles (dim rows of 64 keys, slots swizzled by cm_sig):
+  // the K fragment (kb, kk) takes two transposed reads, each giving lane i
+  // of a 16-lane group dims dbase..dbase+3 of key kbase + i: source lane s
+  // names dim row dbase + (s >> 2) and keys kbase + 4 (s & 3)..+3, with
+  // kbase = 32 kb + 16 (g & 1) and dbase = 16 kk + 8 (g >> 1) (+4 for the
+  // second read), g = lane >> 4. Rows 16 kk + r share cm_sig(r), so kk and
+  // kb only move the address by 2048 kk and flip the chunk bit 2 (64 kb).
+  // The V^T fragment (db, kb, kk) is two 8-byte reads of dim row
+  // 32 db + l32: keys 32 kb + 16 kk + 4 h2 + 0..3 (logical chunk 4 kb + 2 kk,
+  // half h2) and the same 8 keys on (chunk 4 kb + 2 kk + 1), the order of
+  // this lane's probabilities.
+  [[maybe_unused]] uint32_t cka[2] = {0u, 0u};
+  [[maybe_unused]] uint32_t cva = 0u;
+  if constexpr (CM) {
+    const int g = lane >> 4;
+#pragma unroll
+    for (int rd = 0; rd < 2; ++rd) {
+      const int r = 8 * (g >> 1) + 4 * rd + (s16 >> 2);
+      const int c = 2 * (g & 1) + ((s16 & 3) >> 1);
+      cka[rd] = (uint32_t)(r * 128 + 16 * (c ^ cm_sig(r)) + 8 * (s16 & 1));
+    }
+    cva = (uint32_t)(l32 * 128 + 16 * cm_sig(l32) + 8 * h2);
+  }
+
+  // K fragment (kb, kk) of the tile whose K rows start at LDS byte kt_b
+  auto kfrag = [&](uint32_t kt_b, int kb, int kk) -> bf16x8 {
+    if constexpr (CM) {
+      const uint32_t p = kt_b + 2048u * kk;
+      const bf16x4 lo = lds_tr16((p + cka[0]) ^ (64u * kb));
+      const bf16x4 hi = lds_tr16((p + cka[1]) ^ (64u * kb));
+      return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    } else {
+      return lds_ld128(((kt_b + ka0) ^ (32u * kk)) + 32 * kb * kRowB);
+    }
+  };
+
   // S^T = K.Q^T for the tile in `stage` (keys on M, queries on N)
   auto scores = [&](int stage, f32x16 (&s)[2]) {
-    const uint32_t kb0 = ka0 + lds0 + stage * kStage;
+    const uint32_t kt_b = lds0 + stage * kStage;
     s[0] = f32x16{};
     s[1] = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const bf16x8 kf = lds_ld128((kb0 ^ (32u * kk)) + 32 * kb * kRowB);
+        const bf16x8 kf = kfrag(kt_b, kb, kk);
         s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kk], s[kb], 0,
                                                         0, 0);
       }
   };
 
-  // V^T fragment (db, kb, kk) of the tile whose V rows start at vbase
-  auto vfrag = [&](uint32_t vdb, int kb, int kk) {
-    const uint32_t p = vdb + (32 * kb + 16 * kk) * kRowB;
-    const bf16x4 lo = lds_tr16(p);
-    const bf16x4 hi = lds_tr16(p + 8 * kRowB);
-    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  // V^T fragment (db, kb, kk) of the tile whose V rows start at LDS byte
+  // vt_b
+  auto vfrag = [&](uint32_t vt_b, int db, int kb, int kk) -> bf16x8 {
+    if constexpr (CM) {
+      const uint32_t p = vt_b + cva + 4096u * db;
+      const uint32_t c = 4 * kb + 2 * kk;
+      const u32x2 lo = lds_ld64(p ^ (16u * c));
+      const u32x2 hi = lds_ld64(p ^ (16u * (c + 1)));
+      return __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+    } else {
+      const uint32_t p =
+          ((vt_b + va0) ^ (64u * db)) + (32 * kb + 16 * kk) * kRowB;
+      const bf16x4 lo = lds_tr16(p);
+      const bf16x4 hi = lds_tr16(p + 8 * kRowB);
+      return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
   };
 
   // Fused bias rows of this wave's 32 queries: one buffer resource from
@@ -727,15 +832,13 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     // the SIMD's issue port goes to this wave's MFMAs first; the softmax
     // wave fills the slots in between (measured ~2% over equal priority)
     __builtin_amdgcn_s_setprio(1);
-    const uint32_t vb = va0 + lds0 + (t & 3) * kStage + kTileB;
-    const uint32_t kb0 = ka0 + lds0 + ((t + 1) & 3) * kStage;
+    const uint32_t vt_b = lds0 + (t & 3) * kStage + kTileB;
+    const uint32_t kt_b = lds0 + ((t + 1) & 3) * kStage;
     auto vf_n = [&](int n) {
       const int db = n & 3, kb = n >> 3, kk = (n >> 2) & 1;
-      return vfrag(vb ^ (64u * db), kb, kk);
+      return vfrag(vt_b, db, kb, kk);
     };
-    auto kf_n = [&](int n) {
-      return lds_ld128((kb0 ^ (32u * (n >> 1))) + 32 * (n & 1) * kRowB);
-    };
+    auto kf_n = [&](int n) { return kfrag(kt_b, n & 1, n >> 1); };
     // fragments read R - 1 MFMAs ahead; one fewer with the fused bias, whose
     // prefetched values need the registers (the fourth slot made the bias
     // build spill: 2-3% slower on the adapters' shapes)
@@ -930,9 +1033,12 @@ void launch_src(const PrefillArgs& a, int src, dim3 grid, size_t lds,
   else if (src == kPaged)
     hipLaunchKernelGGL((prefill_kernel<REP, REL, kPaged>), grid, dim3(512),
                        lds, st, a);
-  else
+  else if (src == kMixed)
     hipLaunchKernelGGL((prefill_kernel<REP, REL, kMixed>), grid, dim3(512),
                        lds, st, a);
+  else
+    hipLaunchKernelGGL((prefill_kernel<REP, REL, kPackedCM>), grid,
+                       dim3(512), lds, st, a);
 }
 
 template <int REP>
@@ -988,8 +1094,10 @@ extern "C" int tmopt_prefill_check_positions(const int64_t* q_positions,
 
 extern "C" int tmopt_attn_prefill_varlen(
     const void* q, int64_t q_stride_tok, int64_t q_stride_head, const void* k,
-    int64_t k_stride_tok, int64_t k_stride_head, const void* v,
-    int64_t v_stride_tok, int64_t v_stride_head, const int32_t* cu_seqlens_q,
+    int64_t k_stride_run, int64_t k_stride_tok, int64_t k_stride_head,
+    int64_t k_stride_dim, const void* v, int64_t v_stride_run,
+    int64_t v_stride_tok, int64_t v_stride_head, int64_t v_stride_dim,
+    const int32_t* cu_seqlens_q,
     const int32_t* prior_lens, int num_seqs, int max_seqlen_q,
     const void* k_pool, const void* v_pool, const int32_t* block_table,
     int64_t bt_stride, int table_wrap, int page_size, int64_t num_pages,
@@ -1017,7 +1125,7 @@ extern "C" int tmopt_attn_prefill_varlen(
   TMOPT_REQUIRE(rel == nullptr ||
                     (rel_stride_tok >= rel_extent && rel_stride_head >= 0 &&
                      (64 * rel_stride_tok + 2 * (int64_t)rel_extent) <
-                         (1ll << 31)),
+                         kOob),
                 TMOPT_EUNSUPPORTED,
                 "prefill: rel rows must not overlap, and 32 rows must span "
                 "less than 2 GiB (stride_tok=%lld, extent=%d)",
@@ -1032,7 +1140,9 @@ extern "C" int tmopt_attn_prefill_varlen(
   }
   const bool pooled = block_table != nullptr;
   const bool own = k != nullptr || v != nullptr;
-  const int src = !pooled ? kPacked : (own ? kMixed : kPaged);
+  const bool cm = own && (k_stride_dim != 1 || v_stride_dim != 1);
+  const int src = !pooled ? (cm ? kPackedCM : kPacked)
+                          : (own ? kMixed : kPaged);
   if (pooled) {
     TMOPT_REQUIRE(k_pool && v_pool && page_size > 0 && bt_stride > 0 &&
                       num_pages > 0 && table_wrap >= 0,
@@ -1061,19 +1171,52 @@ extern "C" int tmopt_attn_prefill_varlen(
   }
   if (own) {
     TMOPT_REQUIRE(k && v, TMOPT_EINVAL, "prefill: k and v go together");
-    TMOPT_REQUIRE(((int64_t)max_seqlen_q * (k_stride_tok > v_stride_tok
-                                                ? k_stride_tok
-                                                : v_stride_tok) +
-                   kD) * 2 < (1ll << 31),
-                  TMOPT_EUNSUPPORTED,
-                  "prefill: a run's packed k/v span must stay below 2 GiB");
-    TMOPT_REQUIRE(k_stride_tok % 8 == 0 && k_stride_head % 8 == 0 &&
-                      v_stride_tok % 8 == 0 && v_stride_head % 8 == 0 &&
+    TMOPT_REQUIRE(k_stride_run >= 0 && v_stride_run >= 0 &&
+                      k_stride_run % 8 == 0 && v_stride_run % 8 == 0 &&
+                      k_stride_head % 8 == 0 && v_stride_head % 8 == 0 &&
                       ((uintptr_t)k | (uintptr_t)v) % 16 == 0,
                   TMOPT_EINVAL,
-                  "prefill: k/v rows must be 16-byte aligned (strides %% 8)");
+                  "prefill: k/v runs and heads must start 16-byte aligned "
+                  "(run and head strides %% 8)");
+    if (cm) {
+      // channel-major: tokens contiguous, dim rows 16-byte aligned and not
+      // overlapping, runs placed by the run stride (a run's first token
+      // must be 16-byte aligned, which cu_seqlens offsets do not promise)
+      TMOPT_REQUIRE(!pooled, TMOPT_EUNSUPPORTED,
+                    "prefill: channel-major k/v only as the packed source");
+      TMOPT_REQUIRE(k_stride_tok == 1 && v_stride_tok == 1 &&
+                        k_stride_dim != 1 && v_stride_dim != 1,
+                    TMOPT_EINVAL,
+                    "prefill: k and v must both be token-major (stride_dim "
+                    "1) or both channel-major (stride_tok 1)");
+      TMOPT_REQUIRE(k_stride_run > 0 && v_stride_run > 0, TMOPT_EINVAL,
+                    "prefill: channel-major k/v need a run stride");
+      TMOPT_REQUIRE(k_stride_dim % 8 == 0 && v_stride_dim % 8 == 0 &&
+                        k_stride_dim >= max_seqlen_q &&
+                        v_stride_dim >= max_seqlen_q,
+                    TMOPT_EINVAL,
+                    "prefill: channel-major dim rows must be 16-byte aligned "
+                    "and hold max_seqlen_q tokens (stride_dim %% 8, >= %d)",
+                    max_seqlen_q);
+      const int64_t sd = k_stride_dim > v_stride_dim ? k_stride_dim
+                                                     : v_stride_dim;
+      TMOPT_REQUIRE(((kD - 1) * sd + max_seqlen_q) * 2 < kOob,
+                    TMOPT_EUNSUPPORTED,
+                    "prefill: a run's channel-major k/v span must stay below "
+                    "2 GiB");
+    } else {
+      TMOPT_REQUIRE(((int64_t)max_seqlen_q * (k_stride_tok > v_stride_tok
+                                                  ? k_stride_tok
+                                                  : v_stride_tok) +
+                     kD) * 2 < kOob,
+                    TMOPT_EUNSUPPORTED,
+                    "prefill: a run's packed k/v span must stay below 2 GiB");
+      TMOPT_REQUIRE(k_stride_tok % 8 == 0 && v_stride_tok % 8 == 0,
+                    TMOPT_EINVAL,
+                    "prefill: k/v rows must be 16-byte aligned (strides %% 8)");
+    }
   }
-  TMOPT_REQUIRE(((int64_t)max_seqlen_q * q_stride_tok + kD) * 2 < (1ll << 31),
+  TMOPT_REQUIRE(((int64_t)max_seqlen_q * q_stride_tok + kD) * 2 < kOob,
                 TMOPT_EUNSUPPORTED,
                 "prefill: a run's q span must stay below 2 GiB");
   TMOPT_REQUIRE(q_stride_tok % 8 == 0 && q_stride_head % 8 == 0 &&
@@ -1090,6 +1233,10 @@ extern "C" int tmopt_attn_prefill_varlen(
   a.v = (const __bf16*)v;
   a.v_st = v_stride_tok;
   a.v_sh = v_stride_head;
+  a.k_sd = own ? k_stride_dim : 1;
+  a.v_sd = own ? v_stride_dim : 1;
+  a.k_sr = own ? k_stride_run : 0;
+  a.v_sr = own ? v_stride_run : 0;
   a.cu = cu_seqlens_q;
   a.prior = prior_lens;
   a.kpool = (const __bf16*)k_pool;

@@ -441,6 +441,52 @@ def cpu_baseline_c5(wl, reps):
                       f"{n_g} and {st.n_layers - n_g} layers"}
 
 
+# outputs of the adapters' prefill calls, kept for the CPU leg's oracle check
+_PREFILL_NUMERICS = {}
+
+
+def cpu_prefill_numerics(reps=1, rows_per=48):
+    """The adapters' attn_prefill_fused outputs (B=6, T=1536) against the
+    fp32 oracle's model semantics on sampled query rows of every batch row:
+    rel_mean = mean|d| / mean|ref| and the cosine, the reference's arm f
+    (t_fused_prefill_attn.py:284-292; its published 3.824e-3 / 0.999991 are
+    against its eager bf16 chain, ledger.jsonl:29), plus the oracle's time
+    for those rows scaled to the whole call (an estimate)."""
+    from oracle import attn_ref
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    res = {}
+    g = torch.Generator().manual_seed(29)
+    for kind, d in _PREFILL_NUMERICS.items():
+        q, k, v, rel = d["inputs"]
+        B, H, T, D = q.shape
+        fixed = [0, 1, 63, 64, 511, 512, 513, 1023, 1024, 1025, T - 1]
+        rows = sorted(set(fixed + torch.randint(
+            0, T, (rows_per - len(fixed),), generator=g).tolist()))
+        pos = torch.arange(T)
+        ref = None
+
+        def run():
+            nonlocal ref
+            ref = attn_ref.prefill_reference_semantics(
+                q, k, v, rel, pos, d["window"], rows=rows)
+        t, tot, n = _median_time(run, reps)
+        got = d["out"][:, rows].double()
+        ref = ref.double()
+        diff = got - ref
+        res[kind] = {
+            "rel_mean": float(diff.abs().mean() / ref.abs().mean()),
+            "cos": float(torch.nn.functional.cosine_similarity(
+                got.flatten(), ref.flatten(), dim=0)),
+            "max_abs": float(diff.abs().max()),
+            "rows": f"{len(rows)} query rows x {B} batch rows x {H} heads",
+            "reference_b300": {"rel_mean": 3.824e-3, "cos": 0.999991,
+                               "against": "its eager bf16 chain"},
+            "cpu_oracle_s_per_call_estimate": t * T / len(rows),
+            "cores": threads}
+    return res
+
+
 def _rel_band_bytes(n, E, HQ):
     """bf16 bias values a decode row reads: min(visible, E) per head."""
     return int(torch.clamp(n, max=E).sum()) * HQ * 2
@@ -609,6 +655,7 @@ def bench_adapters(tm, wl, steps, warmup, n_sets=2):
     # ---- attn_prefill_fused -----------------------------------------------
     Bp, T = 6, 1536
     ref_ms = {"swa": 1.310, "global": 6.156}   # B300, ledger.jsonl:29
+    ref_peak = {"swa": 2.205, "global": 7.936}
     for kind, HQ, HKV, E, window in (("swa", 64, 16, 512, 512),
                                      ("global", 64, 8, 1024, None)):
         def pf_set():
@@ -627,6 +674,24 @@ def bench_adapters(tm, wl, steps, warmup, n_sets=2):
                                  sets, max(5, steps // 5),
                                  max(2, warmup // 5))
         flops = 4 * D * HQ * wl.visible_pairs([T] * Bp, window or 0)
+        # peak memory of one call, as the reference's arm i measures it
+        # (t_fused_prefill_attn.py:337-344: max_memory_allocated after a
+        # reset, the layer's inputs resident): this call's inputs plus what
+        # the call allocates (the output and the position flag)
+        a0 = sets[0]
+        in_bytes = sum(x.untyped_storage().nbytes() for x in a0[:4])
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        out0 = compat.attn_prefill_fused(*a0)
+        torch.cuda.synchronize()
+        call_bytes = torch.cuda.max_memory_allocated() - base
+        # the oracle's numerics check of this output runs in the CPU leg
+        # (cpu_baselines: rel_mean and cos as the reference's arm f)
+        _PREFILL_NUMERICS[kind] = {
+            "inputs": tuple(x.cpu() for x in a0[:4]), "window": window,
+            "out": out0.cpu()}
+        del out0
         # the same call with token-major K/V ([B, HK, T, D] contiguous):
         # the channel-major source against the row source, same kernel
         tm_sets = [(a[0], a[1].contiguous(), a[2].contiguous()) + a[3:]
@@ -642,7 +707,15 @@ def bench_adapters(tm, wl, steps, warmup, n_sets=2):
             "reference_b300_ms": ref_ms[kind],
             "speedup_vs_reference_b300": ref_ms[kind] / ms,
             "kv_layout": "channel-major (stride 1 along T), read in place",
-            "ms_per_call_token_major_kv": ms_tm}
+            "ms_per_call_token_major_kv": ms_tm,
+            "peak_gib": (in_bytes + call_bytes) / 2**30,
+            "peak_note": "inputs q, k, v, rel of the call plus its own "
+                         "allocations (output, position flag); the "
+                         "reference's 2.205 / 7.936 GiB (ledger.jsonl:29) "
+                         "also hold the rel-mix matmul and tau scaling its "
+                         "timed closure runs (t_fused_prefill_attn.py:"
+                         "310-316), which are outside this call",
+            "reference_b300_peak_gib": ref_peak[kind]}
         res[f"prefill_layer_{kind}_b6_t1536_with_append"] = \
             bench_prefill_append(tm, compat, sets, window, HKV, steps,
                                  warmup)
@@ -755,6 +828,12 @@ def main():
         if args.only == "":
             extra["cpu_baselines"] = cpu_baselines(wl, args.cpu_reps)
             print("[bench] cpu baselines C3/C4/C5 done", file=sys.stderr,
+                  flush=True)
+        if args.only in ("", "adapters") and _PREFILL_NUMERICS:
+            extra.setdefault("adapters", {})["prefill_numerics"] = \
+                cpu_prefill_numerics()
+            _PREFILL_NUMERICS.clear()
+            print("[bench] adapters prefill numerics done", file=sys.stderr,
                   flush=True)
     traffic = measured_traffic()
     line = {

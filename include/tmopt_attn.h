@@ -224,15 +224,36 @@ int tmopt_attn_decode_paged(const void* q, const void* k_pool,
  * kernels read slots and pos in place. Otherwise as
  * tmopt_attn_decode_paged (num_pages = (S+1) * ring_pages), with the same
  * results.
+ * seqs_per_workgroup > 0 replaces the equal page split: work-group i takes
+ * the whole rows [i * seqs_per_workgroup, (i + 1) * seqs_per_workgroup)
+ * (num_workgroups * seqs_per_workgroup >= B, else TMOPT_EINVAL), so no row
+ * is split and the merge launch is skipped (one launch). A row holds at most
+ * ring_pages pages, so with full rings the work stays balanced.
  */
 int tmopt_attn_decode_ring(const void* q, const void* k_pool,
                            const void* v_pool, const int64_t* slots,
                            int ring_pages, const int64_t* pos, int B, int HQ,
                            int HKV, int D, int64_t num_pages, int window,
                            float scale, const void* rel, int rel_extent,
-                           int min_pages, int num_workgroups, void* out,
-                           float* lse, void* workspace,
-                           size_t workspace_bytes, tmopt_stream_t stream);
+                           int min_pages, int num_workgroups,
+                           int seqs_per_workgroup, void* out, float* lse,
+                           void* workspace, size_t workspace_bytes,
+                           tmopt_stream_t stream);
+
+/*
+ * The int32 block table and lengths of attn_global's arguments
+ * (engine/pyengine/kernels/attn_global.py:15-38): flat [B, Lg] int64
+ * per-token pool rows as model.py:938-945 builds them (flat[b, j] =
+ * table[b][j / 16] * 16 + j % 16 for j <= pos[b], 0 beyond) and pos [B]
+ * int64. Writes block_table[b * bt_stride + i] = flat[b, 16 i] / 16 for
+ * i < ceil(Lg / 16) (a page's rows are consecutive, so its first row names
+ * it) and ctx_lens[b] = pos[b] + 1, in one launch: the inputs of
+ * tmopt_attn_decode_paged. bt_stride >= ceil(Lg / 16).
+ */
+int tmopt_decode_table_from_flat(const int64_t* flat, int64_t Lg,
+                                 const int64_t* pos, int B,
+                                 int32_t* block_table, int64_t bt_stride,
+                                 int32_t* ctx_lens, tmopt_stream_t stream);
 
 /*
  * tmopt_attn_decode_paged without the workspace argument: the same kernels

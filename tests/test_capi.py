@@ -116,6 +116,18 @@ def test_invalid_arguments_return_status(tm):
     assert prefill_cm(4 * 128 * 64, 1, 64, 1, 64, table=p) == \
         tm._lib.TMOPT_EUNSUPPORTED
     assert b"only as the packed source" in lib.tmopt_last_error()
+    # ring decode: whole rows per work-group must cover every row
+    rc = lib.tmopt_attn_decode_ring(p, p, p, p, 4, p, 10, 32, 4, 128, 40,
+                                    64, 0.1, null, 0, 8, 3, 3, p, null, p,
+                                    1 << 20, null)
+    assert rc == tm._lib.TMOPT_EINVAL
+    assert b"do not cover" in lib.tmopt_last_error()
+    # table from flat rows: the table row must hold ceil(Lg / 16) pages
+    rc = lib.tmopt_decode_table_from_flat(p, 100, p, 2, p, 6, p, null)
+    assert rc == tm._lib.TMOPT_EINVAL
+    assert b"bt_stride" in lib.tmopt_last_error()
+    assert lib.tmopt_decode_table_from_flat(null, 100, null, 0, null, 0, null,
+                                            null) == 0
     # kv write: misaligned strides
     rc = lib.tmopt_kv_write_slots(p, p, 3, 8, 8, 8, p, 1, 4, 128, p, p, 10,
                                   null)

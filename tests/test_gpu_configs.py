@@ -65,14 +65,3 @@ def test_full_config_every_sequence(tm, dev, config, grid):
     assert_out_close(out, ref_o, what)
     assert_lse_close(lse, ref_l, what)
 
-
-def test_c3_covers_the_window_edges(config):
-    """C3's seeded lengths include sequences shorter than the window, the
-    longest ones, and window starts in the middle of a page."""
-    name, case, _ = config
-    if name != "C3":
-        pytest.skip("C3 only")
-    n = case.ctx_lens.cpu().long()
-    assert int(n.min()) < 4096 < int(n.max())
-    assert int(n.max()) > 30000
-    assert bool((((n - 4096) % 16 != 0) & (n > 4096)).any())

@@ -141,6 +141,63 @@ def test_rel_bias_and_ring_table(tm, dev):
     assert_lse_close(lse, ref_l, "ring+rel")
 
 
+@pytest.mark.parametrize("k,wgs", [(1, 40), (3, 14), (7, 6), (40, 1)])
+def test_ring_whole_rows_per_workgroup(tm, dev, k, wgs):
+    """The ring decode with whole rows per work-group (seqs_per_workgroup:
+    no row split, no merge launch): rows of every fill level (empty, one
+    key, a partial first page, full rings, wrapped rings), B = 40 not a
+    multiple of k, every row and LSE against the oracle; one work-group
+    short of covering B is refused before launch."""
+    g = torch.Generator().manual_seed(31)
+    B, W, HK, D, HQ = 40, 256, 4, 128, 32
+    S = B + 1
+    pool_k = torch.randn((S, W, HK, D), generator=g).to(torch.bfloat16)
+    pool_v = torch.randn((S, W, HK, D), generator=g).to(torch.bfloat16)
+    pos = torch.randint(0, 3 * W, (B,), generator=g)
+    pos[:8] = torch.tensor([0, 1, 15, 16, 255, 256, 700, 40])
+    slots = torch.randperm(B, generator=g)
+    q = torch.randn((B, HQ, D), generator=g).to(torch.bfloat16)
+    rel = (torch.randn((B, HQ, W), generator=g) * 0.5).to(torch.bfloat16)
+    ref_o, ref_l = attn_ref.decode_reference_semantics(q, pool_k, pool_v,
+                                                       slots, pos, rel, W)
+    args = (q.to(dev), pool_k.to(dev), pool_v.to(dev), slots.to(dev),
+            pos.to(dev), 1.0 / D, W)
+    out, lse = tm.decode_ring(*args, rel=rel.to(dev), num_workgroups=wgs,
+                              seqs_per_workgroup=k, return_lse=True)
+    torch.cuda.synchronize()
+    what = f"ring whole rows k={k} wgs={wgs}"
+    assert_out_close(out, ref_o, what)
+    assert_lse_close(lse, ref_l, what)
+    if wgs > 1 and (wgs - 1) * k < B:
+        with pytest.raises(tm.TmoptError):
+            tm.decode_ring(*args, rel=rel.to(dev), num_workgroups=wgs - 1,
+                           seqs_per_workgroup=k)
+
+
+def test_table_from_flat(tm, dev):
+    """attn_global's per-token rows (model.py:938-945) turned into the
+    block table and lengths in one launch: bit-exact against the torch
+    expressions flat[:, ::16] // 16 and pos + 1, for Lg a multiple of 16
+    and not, rows of every length (dead columns 0)."""
+    g = torch.Generator().manual_seed(32)
+    for Lg in (1536, 1500, 17, 1):
+        B = 9
+        npg = (Lg + 15) // 16
+        table_dev = torch.randperm(B * npg * 2, generator=g)[:B * npg].view(
+            B, npg)
+        pos = torch.randint(0, Lg, (B,), generator=g)
+        pos[0] = Lg - 1
+        j = torch.arange(Lg)
+        flat = table_dev[:, j // 16] * 16 + (j % 16)[None]
+        flat = torch.where(j[None] < (pos + 1)[:, None], flat,
+                           torch.zeros((), dtype=torch.int64))
+        table, ctx = tm.decode_table_from_flat(flat.contiguous().to(dev),
+                                               pos.to(dev))
+        torch.cuda.synchronize()
+        assert torch.equal(table.cpu(), (flat[:, ::16] // 16).to(torch.int32))
+        assert torch.equal(ctx.cpu(), (pos + 1).to(torch.int32))
+
+
 def test_empty_and_zero_length(tm, dev):
     """B == 0 is a no-op; a zero-length sequence yields 0 and LSE -inf."""
     from importlib import import_module

@@ -60,3 +60,15 @@ def test_kv_rows_token_major_views():
     one = one.as_strided((1, HK, 8, D), (3, D * 8, 1, 8))
     r = compat._kv_rows(one)
     assert r.data_ptr() == one.data_ptr() and r.stride(0) % 8 == 0
+
+
+def test_c3_lengths_cover_the_window_edges():
+    """Config 3's seeded lengths (the first draw of its generator, as the
+    GPU parity and bench runs make them) include sequences shorter than the
+    window, the longest ones, and window starts in the middle of a page, so
+    the full-size C3 parity test meets every window geometry."""
+    wl = import_module("tm-opt_amd.workloads")
+    n = wl.decode_lens(3, 128, 2048, 32768).long()
+    assert int(n.min()) < 4096 < int(n.max())
+    assert int(n.max()) > 30000
+    assert bool((((n - 4096) % 16 != 0) & (n > 4096)).any())

@@ -21,7 +21,8 @@ from . import _lib
 from ._lib import TmoptError, TmoptLibraryMissing, version
 from .attn import (HEAD_DIM, PAGE_SIZE, decode_default_workgroups,
                    decode_paged, decode_paged_noalloc, decode_ring,
-                   decode_workspace, decode_workspace_size, kv_append_rows,
+                   decode_table_from_flat, decode_workspace,
+                   decode_workspace_size, kv_append_rows,
                    kv_write_paged, kv_write_slots, prefill_check_positions,
                    prefill_varlen)
 from .compat import (attn_global, attn_prefill_chunk_global,
@@ -31,7 +32,8 @@ from .compat import (attn_global, attn_prefill_chunk_global,
 __all__ = [
     "TmoptError", "TmoptLibraryMissing", "version", "HEAD_DIM", "PAGE_SIZE",
     "decode_default_workgroups", "decode_paged", "decode_paged_noalloc",
-    "decode_ring", "decode_workspace", "prefill_check_positions",
+    "decode_ring", "decode_table_from_flat", "decode_workspace",
+    "prefill_check_positions",
     "decode_workspace_size", "kv_append_rows", "kv_write_paged",
     "kv_write_slots",
     "prefill_varlen", "attn_swa", "attn_global", "attn_prefill_fused",

@@ -63,7 +63,9 @@ SIGNATURES = {
     "tmopt_attn_decode_ring": (_c_i32, [
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i32, _c_ptr, _c_i32, _c_i32,
         _c_i32, _c_i32, _c_i64, _c_i32, _c_f32, _c_ptr, _c_i32, _c_i32,
-        _c_i32, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr]),
+        _c_i32, _c_i32, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_ptr]),
+    "tmopt_decode_table_from_flat": (_c_i32, [
+        _c_ptr, _c_i64, _c_ptr, _c_i32, _c_ptr, _c_i64, _c_ptr, _c_ptr]),
     "tmopt_attn_decode_paged_noalloc": (_c_i32, [
         _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i32, _c_ptr, _c_i32,
         _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_f32, _c_ptr,

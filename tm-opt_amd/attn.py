@@ -230,12 +230,14 @@ def decode_paged(q, k_pool, v_pool, block_table, ctx_lens, scale, window=0,
 
 
 def decode_ring(q, pool_k, pool_v, slots, pos, scale, window, rel=None,
-                min_pages=8, num_workgroups=0, out=None, lse=None,
-                workspace=None, return_lse=False):
+                min_pages=8, num_workgroups=0, seqs_per_workgroup=0,
+                out=None, lse=None, workspace=None, return_lse=False):
     """Paged decode over a ring pool as the engine holds it: pool_k/pool_v
     [S, W, HKV, D] bf16 (SwaPool rows), slots [B] int64 ring rows, pos [B]
     int64 query positions, 0 < window <= W; the kernels read slots and pos
     in place (no block table or lengths built per call).
+    seqs_per_workgroup > 0: each work-group takes that many whole rows (no
+    row split, no merge launch; num_workgroups * seqs_per_workgroup >= B).
     Returns (out [B, HQ, D] bf16, lse [B, HQ] fp32 or None).
     Reference: engine/pyengine/kernels/attn_swa.py:120-141, kv.py:215-235."""
     B, HQ, D = q.shape
@@ -263,9 +265,32 @@ def decode_ring(q, pool_k, pool_v, slots, pos, scale, window, rel=None,
               _ptr(slots), per, _ptr(pos), B, HQ, HKV, D, S * per,
               int(window), float(scale), _ptr(rel),
               0 if rel is None else rel.shape[2], int(min_pages),
-              int(num_workgroups), _ptr(out), _ptr(lse), _ptr(workspace),
+              int(num_workgroups), int(seqs_per_workgroup), _ptr(out),
+              _ptr(lse), _ptr(workspace),
               workspace.numel() * workspace.element_size(), _stream(dev))
     return out, lse
+
+
+def decode_table_from_flat(flat, pos, table=None, ctx_lens=None):
+    """attn_global's per-token rows flat [B, Lg] int64 (model.py:938-945)
+    and positions pos [B] int64 -> (block table [B, ceil(Lg/16)] int32 with
+    table[b, i] = flat[b, 16 i] // 16, ctx_lens = pos + 1 int32), one
+    launch. Reference: engine/pyengine/kernels/attn_global.py:15-38."""
+    B, Lg = flat.shape
+    assert flat.dtype == torch.int64 and flat.is_contiguous()
+    assert pos.dtype == torch.int64 and pos.shape == (B,)
+    assert pos.is_contiguous()
+    npg = (Lg + PAGE_SIZE - 1) // PAGE_SIZE
+    dev = flat.device
+    if table is None:
+        table = torch.empty((B, npg), dtype=torch.int32, device=dev)
+    if ctx_lens is None:
+        ctx_lens = torch.empty((B,), dtype=torch.int32, device=dev)
+    assert table.dtype == torch.int32 and table.stride(1) == 1
+    assert table.shape[0] >= B and table.shape[1] >= npg
+    _lib.call("tmopt_decode_table_from_flat", _ptr(flat), Lg, _ptr(pos), B,
+              _ptr(table), table.stride(0), _ptr(ctx_lens), _stream(dev))
+    return table, ctx_lens
 
 
 def decode_paged_noalloc(q, k_pool, v_pool, block_table, ctx_lens, scale,

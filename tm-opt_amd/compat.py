@@ -37,18 +37,18 @@ from . import attn
 PAGE = attn.PAGE_SIZE
 
 
-def _ring_grid(B, HKV, per, dev):
-    """Work split of a ring decode: every sequence holds at most `per`
-    pages, so pieces of k whole rings per work-group (k the fewest that
-    keep to one work-group per compute unit) leave no sequence with full
-    windows split between work-groups. Measured at B = 64, W = 512,
-    64Q/16KV: 52 us against 62 us with the default grid (which splits
-    rings and merges the pieces)."""
+def _ring_grid(B, HKV, dev):
+    """Work split of a ring decode: k whole rings per work-group (k the
+    fewest that keep to one work-group per compute unit), so no row is
+    split between work-groups and the merge launch is skipped. Every row
+    holds at most W/16 pages, so full rings balance exactly. Measured at
+    B = 64, W = 512, 64Q/16KV: 52 us against 62 us with the default grid
+    (which splits rings and merges the pieces). Returns (work-groups, k)."""
     groups = max(1, HKV // 4)
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     per_group = max(1, cus // groups)
     k = -(-B // per_group)
-    return -(-B // k), per * k
+    return -(-B // k), k
 
 
 def attn_swa(q, pool_k, pool_v, slots, pos, rel):
@@ -63,10 +63,10 @@ def attn_swa(q, pool_k, pool_v, slots, pos, rel):
     assert rel.shape == (B, HQ, W), (rel.shape, (B, HQ, W))
     assert slots.dtype == torch.int64 and pos.dtype == torch.int64
     assert W % PAGE == 0, "ring length must be a whole number of pages"
-    wgs, min_pages = _ring_grid(B, HK, W // PAGE, q.device)
+    wgs, k = _ring_grid(B, HK, q.device)
     out, _ = attn.decode_ring(q, pool_k, pool_v, slots.contiguous(),
                               pos.contiguous(), 1.0 / D, W, rel=rel,
-                              min_pages=min_pages, num_workgroups=wgs)
+                              num_workgroups=wgs, seqs_per_workgroup=k)
     return out
 
 
@@ -74,8 +74,9 @@ def attn_global(q, pool_kp, pool_vp, flat, pos, rel, Lg):
     """Global decode attention over a page pool, in place (attn_global.py:15).
     q [B, HQ, D] bf16, pool_kp/pool_vp [(P+1), 16, HK, D] bf16, flat [B, Lg]
     i64 per-token rows (dead columns 0), pos [B] i64, rel [B, HQ, E] bf16.
-    Returns [B, HQ, D]. The block table is recovered from `flat`: rows of
-    one page are consecutive, so page i of row b is flat[b, 16 i] // 16."""
+    Returns [B, HQ, D]. The block table is recovered from `flat` in one
+    launch (rows of one page are consecutive, so page i of row b is
+    flat[b, 16 i] // 16) together with the lengths pos + 1."""
     B, HQ, D = q.shape
     assert q.is_contiguous() and rel.is_contiguous()
     assert pool_kp.is_contiguous() and pool_vp.is_contiguous()
@@ -83,8 +84,7 @@ def attn_global(q, pool_kp, pool_vp, flat, pos, rel, Lg):
     assert flat.dtype == torch.int64 and pos.dtype == torch.int64
     ps = pool_kp.shape[1]
     assert ps == PAGE
-    table = (flat[:, ::ps] // ps).to(torch.int32)
-    ctx = (pos + 1).to(torch.int32)
+    table, ctx = attn.decode_table_from_flat(flat, pos.contiguous())
     out, _ = attn.decode_paged(q, pool_kp, pool_vp, table, ctx, 1.0 / D,
                                window=0, rel=rel, return_lse=False)
     return out

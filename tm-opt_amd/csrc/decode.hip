@@ -95,6 +95,8 @@ struct DecodeArgs {
   const __bf16* rel;
   int rel_extent;
   int min_pages;     // lower bound of pages per work-group
+  int seqs_per_wg;   // > 0: work-group i takes whole sequences
+                     // [i * seqs_per_wg, (i + 1) * seqs_per_wg), no merge
   __bf16* out;
   float* lse;
   float* part_o;     // [B + G, HQ, D] fp32
@@ -290,8 +292,19 @@ void decode_kernel(DecodeArgs a) {
     for (int i = threadIdx.x; i <= a.B; i += blockDim.x) a.geo[1 + i] = pref[i];
     if (threadIdx.x == 0) a.geo[0] = C;
   }
-  const int u0 = min(wg * C, U);
-  const int u1 = min(u0 + C, U);
+  // this work-group's page range: an equal share of the page stream, or
+  // (seqs_per_wg > 0) the pages of whole sequences, so that no sequence is
+  // split and the merge has nothing to do
+  int u0, u1;
+  if (a.seqs_per_wg > 0) {
+    const int b0 = min(wg * a.seqs_per_wg, a.B);
+    const int b1 = min(b0 + a.seqs_per_wg, a.B);
+    u0 = __builtin_amdgcn_readfirstlane(pref[b0]);
+    u1 = __builtin_amdgcn_readfirstlane(pref[b1]);
+  } else {
+    u0 = min(wg * C, U);
+    u1 = min(u0 + C, U);
+  }
   const int hq = kvh * REP + r;  // query head owned as MFMA column r
   const bool head_ok = r < REP;
 
@@ -698,6 +711,22 @@ int scratch_address(void** addr) {
   return TMOPT_OK;
 }
 
+// The block table of attn_global's per-token rows (model.py:938-945: flat
+// [b, j] = table[b][j / 16] * 16 + j % 16 for live j, 0 past the length):
+// table[b][i] = flat[b][16 i] / 16, and ctx_lens[b] = pos[b] + 1. One thread
+// per table entry (entries of pages past a row's length are 0, never read).
+__global__ __launch_bounds__(256) void table_from_flat_kernel(
+    const int64_t* __restrict__ flat, int64_t Lg, const int64_t* __restrict__ pos,
+    int npages, int32_t* __restrict__ table, int64_t table_stride,
+    int32_t* __restrict__ ctx_lens) {
+  const int b = blockIdx.y;
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < npages)
+    table[(int64_t)b * table_stride + i] =
+        (int32_t)(flat[(int64_t)b * Lg + (int64_t)kPS * i] / kPS);
+  if (i == 0) ctx_lens[b] = (int32_t)(pos[b] + 1);
+}
+
 }  // namespace
 }  // namespace tmopt
 
@@ -727,8 +756,8 @@ static int decode_impl(
     int table_wrap, const int32_t* ctx_lens, const int64_t* pos64, int B,
     int HQ, int HKV, int D, int page_size, int64_t num_pages, int window,
     float scale, const void* rel, int rel_extent, int min_pages,
-    int num_workgroups, void* out, float* lse, void* workspace,
-    size_t workspace_bytes, tmopt_stream_t stream) {
+    int num_workgroups, int seqs_per_wg, void* out, float* lse,
+    void* workspace, size_t workspace_bytes, tmopt_stream_t stream) {
   if (B == 0) return TMOPT_OK;
   TMOPT_REQUIRE(B > 0, TMOPT_EINVAL, "decode: B=%d", B);
   TMOPT_REQUIRE(B <= kMaxB, TMOPT_EUNSUPPORTED, "decode: B=%d above %d", B,
@@ -769,6 +798,12 @@ static int decode_impl(
                 TMOPT_EINVAL, "decode: tensors must be 16-byte aligned");
   const int G = num_workgroups > 0 ? num_workgroups : default_wgs(HKV);
   TMOPT_REQUIRE(G <= 65535, TMOPT_EINVAL, "decode: num_workgroups=%d", G);
+  TMOPT_REQUIRE(seqs_per_wg >= 0 &&
+                    (seqs_per_wg == 0 || (int64_t)seqs_per_wg * G >= B),
+                TMOPT_EINVAL,
+                "decode: %d work-groups of %d whole sequences do not cover "
+                "B=%d",
+                G, seqs_per_wg, B);
   size_t off_lse = 0, off_geo = 0;
   const size_t need = ws_layout(B, HQ, G, &off_lse, &off_geo);
   TMOPT_REQUIRE(workspace && workspace_bytes >= need &&
@@ -798,6 +833,7 @@ static int decode_impl(
   a.rel = (const __bf16*)rel;
   a.rel_extent = rel ? rel_extent : 0;
   a.min_pages = min_pages;
+  a.seqs_per_wg = seqs_per_wg;
   a.out = (__bf16*)out;
   a.lse = lse;
   a.part_o = (float*)workspace;
@@ -817,7 +853,7 @@ static int decode_impl(
     default: launch<16>(a, G, nw, lds, st); break;
   }
   int rc = check_launch("decode");
-  if (rc) return rc;
+  if (rc || seqs_per_wg > 0) return rc;   // whole sequences: nothing to merge
   hipLaunchKernelGGL(decode_combine_kernel, dim3(B, (HQ + 7) / 8), dim3(256),
                      0, st, a);
   return check_launch("decode_combine");
@@ -834,7 +870,7 @@ extern "C" int tmopt_attn_decode_paged(
   return decode_impl(0, q, k_pool, v_pool, block_table, nullptr, bt_stride,
                      table_wrap, ctx_lens, nullptr, B, HQ, HKV, D, page_size,
                      num_pages, window, scale, rel, rel_extent, min_pages,
-                     num_workgroups, out, lse, workspace, workspace_bytes,
+                     num_workgroups, 0, out, lse, workspace, workspace_bytes,
                      stream);
 }
 
@@ -843,16 +879,16 @@ extern "C" int tmopt_attn_decode_ring(
     const int64_t* slots, int ring_pages, const int64_t* pos, int B, int HQ,
     int HKV, int D, int64_t num_pages, int window, float scale,
     const void* rel, int rel_extent, int min_pages, int num_workgroups,
-    void* out, float* lse, void* workspace, size_t workspace_bytes,
-    tmopt_stream_t stream) {
+    int seqs_per_workgroup, void* out, float* lse, void* workspace,
+    size_t workspace_bytes, tmopt_stream_t stream) {
   clear_error();
   TMOPT_REQUIRE(ring_pages > 0, TMOPT_EINVAL, "decode_ring: ring_pages=%d",
                 ring_pages);
   return decode_impl(2, q, k_pool, v_pool, nullptr, slots, ring_pages,
                      ring_pages, nullptr, pos, B, HQ, HKV, D, kPS, num_pages,
                      window, scale, rel, rel_extent, min_pages,
-                     num_workgroups, out, lse, workspace, workspace_bytes,
-                     stream);
+                     num_workgroups, seqs_per_workgroup, out, lse, workspace,
+                     workspace_bytes, stream);
 }
 
 extern "C" int tmopt_attn_decode_paged_noalloc(
@@ -881,4 +917,27 @@ extern "C" int tmopt_attn_decode_paged_noalloc(
                                  page_size, num_pages, window, scale, rel,
                                  rel_extent, min_pages, num_workgroups, out,
                                  lse, ws, kScratchBytes, stream);
+}
+
+extern "C" int tmopt_decode_table_from_flat(const int64_t* flat, int64_t Lg,
+                                            const int64_t* pos, int B,
+                                            int32_t* block_table,
+                                            int64_t bt_stride,
+                                            int32_t* ctx_lens,
+                                            tmopt_stream_t stream) {
+  clear_error();
+  if (B == 0) return TMOPT_OK;
+  TMOPT_REQUIRE(B > 0 && B <= 65535 && Lg > 0, TMOPT_EINVAL,
+                "table_from_flat: B=%d Lg=%lld", B, (long long)Lg);
+  TMOPT_REQUIRE(flat && pos && block_table && ctx_lens, TMOPT_EINVAL,
+                "table_from_flat: null pointer");
+  const int64_t npages = (Lg + kPS - 1) / kPS;
+  TMOPT_REQUIRE(npages <= 0x7fffffff && bt_stride >= npages, TMOPT_EINVAL,
+                "table_from_flat: bt_stride=%lld < %lld pages",
+                (long long)bt_stride, (long long)npages);
+  hipLaunchKernelGGL(table_from_flat_kernel,
+                     dim3((unsigned)((npages + 255) / 256), B), dim3(256), 0,
+                     (hipStream_t)stream, flat, Lg, pos, (int)npages,
+                     block_table, bt_stride, ctx_lens);
+  return check_launch("table_from_flat");
 }

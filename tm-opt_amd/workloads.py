@@ -76,6 +76,13 @@ class DecodeCase:
                           dict(self.meta))
 
 
+def decode_lens(index, B, lo, hi, g=None):
+    """The context lengths of a seeded decode config: the first draw of its
+    generator, U{lo..hi} (make_decode's order: lengths, table, Q, K, V)."""
+    g = generator(index, "cpu") if g is None else g
+    return torch.randint(lo, hi + 1, (B,), generator=g)
+
+
 def make_decode(name, index, B, lo, hi, window=0, device="cpu",
                 poison=True, hq=HQ, hkv=HKV, ctx=None, pool_factor=2):
     """Paged decode batch: ctx ~ U{lo..hi} (or the given list), pages of the
@@ -84,7 +91,7 @@ def make_decode(name, index, B, lo, hi, window=0, device="cpu",
     page point at one NaN poison page (never to be read)."""
     g = generator(index, "cpu")
     if ctx is None:
-        ctx = torch.randint(lo, hi + 1, (B,), generator=g)
+        ctx = decode_lens(index, B, lo, hi, g)
     else:
         ctx = torch.as_tensor(ctx, dtype=torch.int64)
     n_log = (ctx + PAGE - 1) // PAGE                 # logical pages

@@ -204,12 +204,12 @@ def bench_mixed(tm, wl, steps, warmup):
     # the step's decode grid is sized to share the chip with the prefill;
     # the stand-alone grid (the library default) gives the kernel's own rate
     B, HQ, _ = st.q_decode.shape
-    HKV = st.pool_g[0].shape[2]
+    HKV = st.pools[0][0].shape[2]
     ws_full = tm.decode_workspace(B, HQ, HKV, st.q_decode.device)
     n_chunks = len(st.chunk_lens)
 
     def decode_full(l):
-        kp, vp = st.pool_g if st.is_global[l] else st.pool_s
+        kp, vp = st.pool(l)
         tm.decode_paged(st.q_decode, kp, vp, st.tables[l][n_chunks:],
                         st.dec_ctx, st.scale,
                         window=0 if st.is_global[l] else st.window,
@@ -392,7 +392,7 @@ def cpu_baselines(wl, reps=3):
 def _layer_to_cpu(st, layer):
     """CPU copy of one config-5 layer's pages (those its table rows
     reference), with the table renumbered to them."""
-    kp, vp = st.pool_g if st.is_global[layer] else st.pool_s
+    kp, vp = st.pool(layer)
     t = st.tables[layer].long()
     pages = torch.unique(t)
     remap = torch.full((kp.shape[0],), -1, dtype=torch.long, device=t.device)

@@ -24,7 +24,7 @@ def step(dev):
 
 def _rows(step, l, rows):
     """Compact CPU copy of the pages the given table rows reference."""
-    kp, vp = step.pool_g if step.is_global[l] else step.pool_s
+    kp, vp = step.pool(l)
     t = step.tables[l][rows].long()
     pages = torch.unique(t)
     remap = torch.full((kp.shape[0],), -1, dtype=torch.long,
@@ -70,7 +70,7 @@ def test_config5_layer_sampled(tm, dev, step, layer):
                                V.repeat_interleave(rep, 1))
             assert_out_close(outp[r], ref, f"C5 L{layer} chunk{c} q{j}")
     # the appended tokens landed where the table says (bit-exact)
-    kp, _ = step.pool_g if step.is_global[layer] else step.pool_s
+    kp, _ = step.pool(layer)
     t = step.tables[layer]
     for r, tok in ((0, 0), (1, 2047), (nc + 7, None)):
         pos = int(step.start_all[r]) + (0 if tok is None else tok)

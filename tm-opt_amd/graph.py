@@ -147,7 +147,7 @@ class MixedStepGraph:
         self.s = step
         dev = step.q_decode.device
         B, HQ, D = step.q_decode.shape
-        HKV = step.pool_g[0].shape[2]
+        HKV = step.pools[0][0].shape[2]
         if overlap and num_workgroups == 0:
             num_workgroups = max(
                 1, attn.decode_default_workgroups(HKV) * 2 // 3)
@@ -164,7 +164,7 @@ class MixedStepGraph:
 
     def layer(self, l, parts=("kv", "prefill", "decode")):
         s = self.s
-        kp, vp = s.pool_g if s.is_global[l] else s.pool_s
+        kp, vp = s.pool(l)
         w = 0 if s.is_global[l] else s.window
         t = s.tables[l]
         if "kv" in parts:

@@ -252,16 +252,16 @@ def paged_layout(lens, g, pool_factor=2, prior=None):
 class MixedStep:
     """One step of config 5 for every layer. Rows 0..n_chunks-1 of each
     layer's block table are the chunked-prefill runs, the rest the decode
-    rows. Each layer walks its own shuffled table over one physical pool per
-    layer kind (global / sliding window): a layer's footprint (GBs) is far
-    above the 256 MB Infinity Cache, so its HBM traffic equals that of a
-    private pool."""
+    rows. Every layer has a pool set of its own (K and V pages of a global
+    layer: every page of every row; of a window layer: the pages a query of
+    the row can see) and a shuffled table over it, so no layer reads pages
+    another layer has just brought into the 256 MB Infinity Cache: ~88 GB
+    of pools in all."""
     n_layers: int
     window: int
     is_global: list             # per layer
     tables: list                # per layer [R, width] int32
-    pool_g: tuple               # (k, v) [Pg, 16, HKV, D]
-    pool_s: tuple
+    pools: list                 # per layer (k, v) [P_l, 16, HKV, D]
     chunk_lens: list
     chunk_prior: list
     dec_ctx: torch.Tensor       # [96] int32 (after this step's append)
@@ -276,12 +276,16 @@ class MixedStep:
     scale: float = SCALE
     meta: dict = field(default_factory=dict)
 
+    def pool(self, layer):
+        """(k, v) page pools of one layer."""
+        return self.pools[layer]
+
     def decode_bytes(self, layer):
         n = self.dec_ctx.to(torch.int64).cpu()
         if not self.is_global[layer]:
             n = torch.minimum(n, torch.tensor(self.window))
         B, hq, d = self.q_decode.shape
-        hkv = self.pool_g[0].shape[2]
+        hkv = self.pools[0][0].shape[2]
         return int(n.sum()) * hkv * d * 4 + B * hq * d * 4 + B * hq * 4 + \
             int(((n + PAGE - 1) // PAGE).sum()) * 4 + B * 4
 
@@ -323,8 +327,8 @@ def config5(device="cuda", n_layers=66, window=4096, n_decode=96,
         v = _randn_bf16((P, PAGE, hkv, D), gd, device)
         return k, v
 
-    pool_g, pool_s = pool(Pg), pool(Ps)
     is_global = [i % 4 == 3 for i in range(n_layers)]
+    pools = [pool(Pg if is_global[i] else Ps) for i in range(n_layers)]
     tables = []
     for i in range(n_layers):
         P = Pg if is_global[i] else Ps
@@ -345,7 +349,7 @@ def config5(device="cuda", n_layers=66, window=4096, n_decode=96,
     ic = lambda x: torch.tensor(x, dtype=torch.int32, device=device)
     return MixedStep(
         n_layers=n_layers, window=window, is_global=is_global, tables=tables,
-        pool_g=pool_g, pool_s=pool_s, chunk_lens=[chunk] * n_chunks,
+        pools=pools, chunk_lens=[chunk] * n_chunks,
         chunk_prior=[prior] * n_chunks, dec_ctx=ctx.to(torch.int32).to(device),
         q_prefill=_randn_bf16((n_chunks * chunk, HQ, D), gd, device),
         q_decode=_randn_bf16((n_decode, HQ, D), gd, device),

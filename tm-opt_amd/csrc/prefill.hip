@@ -80,43 +80,17 @@ __device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
 
 // 16 bytes per lane from global memory straight into LDS: lane l of the
 // wave writes bytes lds + 16 l .. +15. Issued from inline assembly so that
-// the compiler does not wait for it at every barrier; the kernel waits for
-// these loads itself (wait_vm).
-__device__ __forceinline__ void dma_b128(i32x4 rsrc, uint32_t lds, int voff) {
+// the compiler does not wait for it at every barrier or before LDS reads it
+// cannot prove disjoint from it; the kernel waits for these loads itself
+// (wait_vm). The compiler's own waits for ordinary loads (the fused bias)
+// do not count these: they wait for every DMA issued between the load and
+// its use, so the tile loop issues no DMA in that stretch.
+__device__ __forceinline__ void dma(i32x4 rsrc, uint32_t lds, int voff) {
   asm volatile(
       "s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
       :
       : "s"(lds), "v"(voff), "s"(rsrc)
       : "memory", "m0");
-}
-
-// The same DMA through the compiler's LDS-DMA builtin, so that the
-// compiler counts it among the wave's outstanding loads. Used where the
-// tile loop also issues ordinary loads (the fused bias): their waits are
-// then counted past the DMA instead of draining it. The compiler in turn
-// waits for the DMA before LDS reads it cannot prove disjoint from it;
-// on the bias shapes both forms measured the same (within 2%).
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-
-template <bool VIS>
-__device__ __forceinline__ auto mk_rsrc(const void* base, uint32_t bytes) {
-  if constexpr (VIS)
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base),
-                                             (short)0, (int)bytes,
-                                             0x00020000);
-  else
-    return make_rsrc(base, bytes);
-}
-
-// (overloads on the resource type: the builtin's resource type cannot be
-// a deduced template parameter)
-__device__ __forceinline__ void dma(rsrc_t rsrc, uint32_t lds, int voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      rsrc, (__attribute__((address_space(3))) void*)(uintptr_t)lds, 16,
-      (unsigned)voff, 0, 0, 0);
-}
-__device__ __forceinline__ void dma(i32x4 rsrc, uint32_t lds, int voff) {
-  dma_b128(rsrc, lds, voff);
 }
 
 // wait until at most N vector-memory loads of this wave are in flight
@@ -352,8 +326,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   const uint32_t lds0 =
       (uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)smem);
   // packed rows of the run (keys 0.. of the run itself)
-  constexpr bool VIS = REL;   // DMA the compiler can see (see dma())
-  auto rk = mk_rsrc<VIS>(nullptr, 0u), rv = mk_rsrc<VIS>(nullptr, 0u);
+  i32x4 rk = make_rsrc(nullptr, 0u), rv = make_rsrc(nullptr, 0u);
   int kst_b = 0, vst_b = 0, klane_p = 0, vlane_p = 0;
   [[maybe_unused]] int cm_key = 0;
   if constexpr (OWN) {
@@ -372,9 +345,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
       // outside the resource and arrive as zeros.
       kst_b = (int)(a.k_sd * 2);
       vst_b = (int)(a.v_sd * 2);
-      rk = mk_rsrc<VIS>(a.k + k0 + (int64_t)kvh * a.k_sh,
+      rk = make_rsrc(a.k + k0 + (int64_t)kvh * a.k_sh,
                         (uint32_t)(((int64_t)(kD - 1) * a.k_sd + len) * 2));
-      rv = mk_rsrc<VIS>(a.v + v0 + (int64_t)kvh * a.v_sh,
+      rv = make_rsrc(a.v + v0 + (int64_t)kvh * a.v_sh,
                         (uint32_t)(((int64_t)(kD - 1) * a.v_sd + len) * 2));
       const int r = 8 * w + (lane >> 3);
       const int c = (lane & 7) ^ cm_sig(r);
@@ -384,9 +357,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     } else {
       kst_b = (int)(a.k_st * 2);
       vst_b = (int)(a.v_st * 2);
-      rk = mk_rsrc<VIS>(a.k + k0 + (int64_t)kvh * a.k_sh,
+      rk = make_rsrc(a.k + k0 + (int64_t)kvh * a.k_sh,
                         (uint32_t)(((int64_t)(len - 1) * a.k_st + kD) * 2));
-      rv = mk_rsrc<VIS>(a.v + v0 + (int64_t)kvh * a.v_sh,
+      rv = make_rsrc(a.v + v0 + (int64_t)kvh * a.v_sh,
                         (uint32_t)(((int64_t)(len - 1) * a.v_st + kD) * 2));
       klane_p = grp * kst_b + 16 * kchunk;
       vlane_p = grp * vst_b + 16 * vchunk;
@@ -413,7 +386,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // and so does a page whose table entry lies outside the pool or past the
   // row's width. The lane offset is relative to the resource base, so the
   // rows below it have negative offsets, i.e. out of range.
-  auto pool_dma = [&](int key0, uint32_t dk, uint32_t dv) {
+  // (live == false: the same instructions with an offset past every
+  // resource, so nothing is fetched and the stage gets zeros)
+  auto pool_dma = [&](int key0, uint32_t dk, uint32_t dv, bool live) {
     if constexpr (POOL) {
       const int lp = key0 >> 4;
       const int col = a.table_wrap > 0 ? lp % a.table_wrap : lp;
@@ -424,32 +399,36 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
       const uint32_t nrec = valid ? (uint32_t)((r_hi - r_lo) * row_b) : 0u;
       const int64_t pofs = valid ? (int64_t)pg * page_b + r_lo * row_b : 0;
       const int roff = ((key0 & (kPage - 1)) - r_lo) * row_b;
-      dma(mk_rsrc<VIS>(reinterpret_cast<const char*>(a.kpool) + pofs,
+      dma(make_rsrc(reinterpret_cast<const char*>(a.kpool) + pofs,
                             nrec),
-               dk, klane + roff);
-      dma(mk_rsrc<VIS>(reinterpret_cast<const char*>(a.vpool) + pofs,
+               dk, live ? klane + roff : kOob);
+      dma(make_rsrc(reinterpret_cast<const char*>(a.vpool) + pofs,
                             nrec),
-               dv, vlane + roff);
+               dv, live ? vlane + roff : kOob);
     }
   };
   // four packed rows j..j+3 of the run's own keys into LDS (rows past the
   // run end are outside the resource: zeros)
-  auto own_dma = [&](int j, uint32_t dk, uint32_t dv) {
+  auto own_dma = [&](int j, uint32_t dk, uint32_t dv, bool live) {
     if constexpr (OWN) {
-      dma(rk, dk, klane_p + j * kst_b);
-      dma(rv, dv, vlane_p + j * vst_b);
+      dma(rk, dk, live ? klane_p + j * kst_b : kOob);
+      dma(rv, dv, live ? vlane_p + j * vst_b : kOob);
     }
   };
 
   // issue tile `t` (index from k_lo) into LDS stage `st`: 4 instructions
   // per wave (2 with the source split inside a 4-row block: one per source,
-  // each under the exec mask of the lanes whose row it holds)
-  auto issue_tile = [&](int t, int st) {
+  // each under the exec mask of the lanes whose row it holds). live ==
+  // false issues the same instructions fetching nothing: the loops issue a
+  // tile every iteration, past the last one too, so that the wave's count
+  // of loads in flight is the same on every path and the waits at the end
+  // of the odd slots are exact.
+  auto issue_tile = [&](int t, int st, bool live = true) {
     const int kt = k_lo + t * kBN;
     const uint32_t sb = lds0 + st * kStage;
     if constexpr (CM) {
       // dim rows 8w.. and 64+8w.. of the channel-major tile (see above)
-      const bool in = kt + cm_key < len;
+      const bool in = live && kt + cm_key < len;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const uint32_t dk = sb + (w + 8 * i) * 1024, dv = dk + kTileB;
@@ -463,18 +442,18 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         const uint32_t dk = sb + r0 * kRowB, dv = dk + kTileB;
         const int key0 = kt + r0;
         if constexpr (SRC == kPacked) {
-          own_dma(key0, dk, dv);
+          own_dma(key0, dk, dv, live);
         } else if constexpr (SRC == kPaged) {
-          pool_dma(key0, dk, dv);
+          pool_dma(key0, dk, dv, live);
         } else {
           if (key0 + 4 <= plim) {
-            pool_dma(key0, dk, dv);
+            pool_dma(key0, dk, dv, live);
           } else if (key0 >= plim) {
-            own_dma(key0 - plim, dk, dv);
+            own_dma(key0 - plim, dk, dv, live);
           } else {
             // lane group grp holds row key0 + grp
-            if (key0 + grp < plim) pool_dma(key0, dk, dv);
-            else own_dma(key0 - plim, dk, dv);
+            if (key0 + grp < plim) pool_dma(key0, dk, dv, live);
+            else own_dma(key0 - plim, dk, dv, live);
           }
         }
       }
@@ -599,7 +578,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // the whole offset goes in the lane register, where the check sees it.
   // Every call issues exactly 8 loads (a tile outside the band or past the
   // run reads nothing), so the wave's load counts stay fixed: the waits
-  // for them never reach the tile DMA issued after them.
+  // at the end of the odd slots count them exactly.
   typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
   [[maybe_unused]] u32x3 rb[8];
   [[maybe_unused]] auto bias_issue = [&](int kt) {
@@ -774,13 +753,20 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   bf16x8 pf[2][2];     // probabilities of the tile being multiplied
 
   // softmax of scores `s` of the tile at kt (masking when needed): P^T
-  // fragments, running max / sum update, O^T rescale when the max moved
-  auto softmax_phase = [&](f32x16 (&s)[2], int kt, bool first) {
+  // fragments, running max / sum update, O^T rescale when the max moved.
+  // `hook` runs once the tile's bias loads have arrived (the fused-bias
+  // loops issue their tile DMA there, past the compiler's wait for them).
+  auto softmax_phase = [&](f32x16 (&s)[2], int kt, bool first, auto&& hook) {
     // the bias band: some pair of the tile has dist = q - k < E (the
     // smallest dist is pos_lo - (kt + 63))
     const bool with_bias = REL && pos_lo - (kt + kBN - 1) < a.rel_extent;
     const bool full = full_tile(kt);
     if constexpr (REL) {
+      // every tile waits for its bias loads here, used or not, so that no
+      // load into a dead register is left in flight to be waited for
+      // later (past the tile DMA issued by `hook` below)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(rb[i]));
       if (with_bias) {
         if (full && pos_hi - kt < a.rel_extent)
           bias_apply(s, kt, std::true_type{});
@@ -788,6 +774,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
           bias_apply(s, kt, std::false_type{});
       }
     }
+    hook();
     if (!full) mask_tile(s, kt);
     const float sl2 = with_bias ? kLog2e : a.scale_log2;
     float mx = -INFINITY;
@@ -886,7 +873,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   {
     const int qrow0 = q0 + 32 * (w % QSUB);
     const int64_t qspan = ((int64_t)(len - qrow0 - 1) * a.q_st + kD) * 2;
-    const auto rq = mk_rsrc<VIS>(
+    const auto rq = make_rsrc(
         a.q + (int64_t)(t0 + qrow0) * a.q_st + (int64_t)head * a.q_sh,
         qrow0 < len ? (uint32_t)qspan : 0u);
     const int qst_b = (int)(a.q_st * 2);
@@ -914,8 +901,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // before the barrier that publishes it. Loads issued after that tile's
   // may still fly: the DMA of tile t+3 and, with the fused bias, the bias
   // loads of the tile after the next softmax (`bias` of them).
-  auto odd_end = [&](int t, int bias) {
-    const int n = (t + 3 < ntiles ? 4 : 0) + bias;
+  auto odd_end = [&](int n_dma, int bias) {
+    const int n = n_dma + bias;
     if (n == 12) wait_vm<12>();
     else if (n == 8) wait_vm<8>();
     else if (n == 4) wait_vm<4>();
@@ -923,53 +910,62 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     __syncthreads();
   };
   constexpr int NB = REL ? 8 : 0;   // bias loads per tile
+  // With the fused bias a wave issues its tile DMA inside its softmax, right
+  // after the wait for that tile's bias loads, and not before: group 0 in
+  // slot 2t+1, group 1 in slot 2t (tile t+3's stage is free from slot 2t
+  // on; the DMA then lands over the next one to two slots).
   // The first and last tiles are peeled off the loops, so that the loops
   // hold one variant of the MFMA phase: O^T then keeps one set of
   // registers across iterations (variants merged inside the loop made the
   // compiler copy all 64 accumulator registers back and forth every tile).
   constexpr std::true_type kWithS{};
   constexpr std::false_type kNoS{};
+  auto none = [] {};
   if (grp_id == 0) {
     scores(0, sc);
     bias_issue(k_lo);
-    softmax_phase(sc, k_lo, true);
+    softmax_phase(sc, k_lo, true, none);
     bias_issue(k_lo + kBN);
     for (int t = 0; t + 1 < ntiles; ++t) {
-      if (t + 3 < ntiles) issue_tile(t + 3, (t + 3) & 3);
+      if constexpr (!REL) issue_tile(t + 3, (t + 3) & 3, t + 3 < ntiles);
       mfma_phase(t, kWithS);
       __syncthreads();
-      softmax_phase(sc, k_lo + (t + 1) * kBN, false);
+      softmax_phase(sc, k_lo + (t + 1) * kBN, false, [&] {
+        if constexpr (REL) issue_tile(t + 3, (t + 3) & 3, t + 3 < ntiles);
+      });
       bias_issue(k_lo + (t + 2) * kBN);
-      odd_end(t, NB);
+      odd_end(4, NB);
     }
     mfma_phase(ntiles - 1, kNoS);
     __syncthreads();
-    odd_end(ntiles - 1, 0);
+    odd_end(0, 0);   // everything, before the output goes through LDS
   } else {
-    if (3 < ntiles) issue_tile(3, 3);
+    if constexpr (!REL) issue_tile(3, 3, 3 < ntiles);
     scores(0, sc);
     bias_issue(k_lo);
-    softmax_phase(sc, k_lo, true);
+    softmax_phase(sc, k_lo, true, [&] {
+      if constexpr (REL) issue_tile(3, 3, 3 < ntiles);
+    });
     bias_issue(k_lo + kBN);
     __syncthreads();
     if (ntiles > 1) mfma_phase(0, kWithS);
     else mfma_phase(0, kNoS);
-    odd_end(0, NB);
+    odd_end(ntiles > 1 ? 4 : 0, NB);
     for (int t = 1; t + 1 < ntiles; ++t) {
-      if (t + 3 < ntiles) issue_tile(t + 3, (t + 3) & 3);
-      softmax_phase(sc, k_lo + t * kBN, false);
+      softmax_phase(sc, k_lo + t * kBN, false,
+                    [&] { issue_tile(t + 3, (t + 3) & 3, t + 3 < ntiles); });
       bias_issue(k_lo + (t + 1) * kBN);
       __syncthreads();
       mfma_phase(t, kWithS);
-      odd_end(t, NB);
+      odd_end(4, NB);
     }
     if (ntiles > 1) {
       const int t = ntiles - 1;
-      softmax_phase(sc, k_lo + t * kBN, false);
+      softmax_phase(sc, k_lo + t * kBN, false, none);
       bias_issue(k_lo + (t + 1) * kBN);
       __syncthreads();
       mfma_phase(t, kNoS);
-      odd_end(t, NB);
+      odd_end(0, NB);   // the tile loads, before the output goes through LDS
     }
   }
   }  // !rejected

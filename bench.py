@@ -515,12 +515,15 @@ class _BenchRing:
 
 def bench_prefill_append(tm, compat, sets, window, HKV, steps, warmup):
     """One prefill layer's cache population + attention, as the engine runs
-    it (model.py:507-528), two ways: (a) the append of every row from the
+    it (model.py:507-528), three ways: (a) the append of every row from the
     sconv's channel-major K/V (read in place) followed by
     attn_prefill_fused (which reads the same K/V in place); (b)
-    attn_prefill_fused given the caches (append inside; a global layer then
-    reads its keys from the pages just written, an SWA layer from the K/V
-    tensors). a - b is what the batched path removes."""
+    attn_prefill_fused given the caches (the same two launches from one
+    call); (c) as (a) but with a token-major copy of K and V made first, what
+    a prefill that needs head_dim-contiguous rows pays. c - b is what reading
+    the channel-major K/V in place removes. SWA caches are rings that are
+    rows of one pool (SwaPool, kv.py:231-245), global ones pages of one pool
+    (GlobalPool): one append launch per layer either way."""
     q0, k0 = sets[0][0], sets[0][1]
     Bp, H, T, D = q0.shape
     npg = (T + 15) // 16
@@ -532,13 +535,15 @@ def bench_prefill_append(tm, compat, sets, window, HKV, steps, warmup):
     rows = [torch.zeros(npg, dtype=torch.int64, device=dev)
             for _ in range(Bp)]
     W = window or 0
-    rings = [[(torch.empty((W, HKV, D), dtype=torch.bfloat16, device=dev),
-               torch.empty((W, HKV, D), dtype=torch.bfloat16, device=dev))
-              for _ in range(Bp)] for _ in sets] if window else None
+    rings = [(torch.empty((Bp + 1, W, HKV, D), dtype=torch.bfloat16,
+                          device=dev),
+              torch.empty((Bp + 1, W, HKV, D), dtype=torch.bfloat16,
+                          device=dev)) for _ in sets] if window else None
 
     def caches(si):
         if window:
-            return [_BenchRing(*r) for r in rings[si]]
+            rk, rv = rings[si]
+            return [_BenchRing(rk[b], rv[b]) for b in range(Bp)]
         free = list(range(P))
         return [_BenchPages(pools[si][0], pools[si][1], free, rows[b])
                 for b in range(Bp)]
@@ -554,18 +559,39 @@ def bench_prefill_append(tm, compat, sets, window, HKV, steps, warmup):
     def fused(a):
         compat.attn_prefill_fused(*a, caches=caches(order[id(a)]))
 
-    _, ms_a = time_launches(separate, sets, max(5, steps // 5),
-                            max(2, warmup // 5))
-    _, ms_b = time_launches(fused, sets, max(5, steps // 5),
-                            max(2, warmup // 5))
+    def packed(a):
+        cs = caches(order[id(a)])
+        kr, vr = compat._kv_rows(a[1]), compat._kv_rows(a[2])
+        compat._append_rows(kr, vr, cs, [T] * Bp)
+        kt = kr.contiguous().transpose(1, 2)     # token-major copies
+        vt = vr.contiguous().transpose(1, 2)
+        compat.attn_prefill_fused(a[0], kt, vt, *a[3:])
+
+    def pages_only(a):
+        # the cache objects' own page allocation (PagedKV.ensure_pages,
+        # kv.py:170-191: free-list pops and a device mirror of the new ids
+        # per row), which every path above pays
+        for c in caches(order[id(a)]):
+            if hasattr(c, "ensure_pages"):
+                c.ensure_pages(npg - 1)
+
+    n, w = max(5, steps // 5), max(2, warmup // 5)
+    _, ms_a = time_launches(separate, sets, n, w)
+    _, ms_b = time_launches(fused, sets, n, w)
+    _, ms_c = time_launches(packed, sets, n, w)
+    _, ms_p = time_launches(pages_only, sets, n, w)
     kv_bytes = 2 * Bp * HKV * T * D * 2
     return {"ms_append_then_attention": ms_a,
             "ms_attention_with_caches": ms_b,
-            "ms_removed": ms_a - ms_b,
+            "ms_append_copy_then_attention": ms_c,
+            "ms_removed": ms_c - ms_b,
+            "ms_cache_page_allocation": ms_p,
             "kv_bytes_per_call": kv_bytes,
-            "note": "K/V channel-major, read in place by the append and "
-                    "the prefill (no packed copy on either path); global: "
-                    "keys read back from the pages just written"}
+            "note": "K/V channel-major as the sconv hands them over; a, b "
+                    "read them in place (append and attention), c copies "
+                    "them token-major first; ms_removed = c - b; "
+                    "ms_cache_page_allocation: the page caches' own "
+                    "ensure_pages (part of a, b, c; none for rings)"}
 
 
 def bench_adapters(tm, wl, steps, warmup, n_sets=2):

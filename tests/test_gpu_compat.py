@@ -147,16 +147,18 @@ def test_positions_check_lengths(tm, dev):
 
 
 @pytest.mark.parametrize("T,lens", [(200, [200, 150, 77]), (77, [77, 60, 5])])
-@pytest.mark.parametrize("kind", ["global", "swa"])
+@pytest.mark.parametrize("kind", ["global", "swa", "swa_pooled"])
 def test_attn_prefill_fused_populates_caches(tm, dev, kind, T, lens):
     """attn_prefill_fused given the rows' caches (the engine's
     st.cache.append(kn[i, :lens[i]], vv[i, :lens[i]]) at model.py:507-512)
-    appends the channel-major K/V itself; a global layer then reads its keys
-    back from the pages, an SWA layer reads the K/V tensors and fills its
-    rings. The live rows equal the cache-less path's bitwise, every cache
-    holds its row's tokens bit-exact, n advances. T = 77: channel-major dim
-    rows that are not 16-byte aligned, which neither kernel reads in place:
-    the adapter copies them before it touches any cache."""
+    appends the channel-major K/V itself (pages of a shared pool, separate
+    rings, or rings that are rows of one SwaPool in a permuted slot order,
+    kv.py:231-245) and reads the K/V tensors for the attention. The live
+    rows equal the cache-less path's bitwise, every cache holds its row's
+    tokens bit-exact, n advances, pool rows no cache owns stay untouched.
+    T = 77: channel-major dim rows that are not 16-byte aligned, which
+    neither kernel reads in place: the adapter copies them before it
+    touches any cache."""
     import numpy as np
     from helpers import PagedCache, RingCache
     from oracle import kv_ref
@@ -183,26 +185,38 @@ def test_attn_prefill_fused_populates_caches(tm, dev, kind, T, lens):
         vp = torch.zeros_like(kp)
         caches = [PagedCache(kp, vp, free, torch.zeros(
             P // 2, dtype=torch.int64, device=dev)) for _ in range(B)]
-    else:
+    elif kind == "swa":
         caches = [RingCache(torch.zeros((E, hk, D), dtype=bf, device=dev),
                             torch.zeros((E, hk, D), dtype=bf, device=dev))
                   for _ in range(B)]
+    else:
+        pk = torch.zeros((B + 2, E, hk, D), dtype=bf, device=dev)
+        pv = torch.zeros_like(pk)
+        slots = [3, 0, 2]
+        caches = [RingCache(pk[s], pv[s]) for s in slots]
     out = tm.attn_prefill_fused(q, k, v, rel, ar, ar, window, caches=caches,
                                 lens=lens)
     torch.cuda.synchronize()
+    if kind == "swa_pooled":
+        for s in (1, 4):
+            assert not bool(pk[s].any()) and not bool(pv[s].any()), s
     for i, n in enumerate(lens):
         assert torch.equal(out[i, :n], base[i, :n]), f"row {i}"
         c = caches[i]
         assert c.n == n
-        rows = k[i].transpose(0, 1)[:n].contiguous()             # [n, hk, D]
-        if kind == "global":
-            got = kv_ref.gather(kv_ref.as_u16(c.kp), c.table, n)
-        else:
-            got = kv_ref.gather(kv_ref.as_u16(c.k).reshape(E // 16, 16, hk, D),
-                                list(range(E // 16)), n,
-                                table_wrap=E // 16, lo=max(0, n - E))
-            rows = rows[max(0, n - E):]
-        assert np.array_equal(got, kv_ref.as_u16(rows)), f"cache row {i}"
+        for x, pool, ring in ((k, "kp", "k"), (v, "vp", "v")):
+            rows = x[i].transpose(0, 1)[:n].contiguous()         # [n, hk, D]
+            if kind == "global":
+                got = kv_ref.gather(kv_ref.as_u16(getattr(c, pool)), c.table,
+                                    n)
+            else:
+                got = kv_ref.gather(
+                    kv_ref.as_u16(getattr(c, ring)).reshape(E // 16, 16, hk, D),
+                    list(range(E // 16)), n, table_wrap=E // 16,
+                    lo=max(0, n - E))
+                rows = rows[max(0, n - E):]
+            assert np.array_equal(got, kv_ref.as_u16(rows)), \
+                f"cache row {i} ({ring})"
 
 
 def test_attn_swa_model_shape_ring_grid(tm, dev):

@@ -72,3 +72,35 @@ def test_c3_lengths_cover_the_window_edges():
     assert int(n.min()) < 4096 < int(n.max())
     assert int(n.max()) > 30000
     assert bool((((n - 4096) % 16 != 0) & (n > 4096)).any())
+
+
+def test_ring_pool_detects_swapool_rows():
+    """Rings that are rows of one SwaPool tensor (the engine's pooled
+    RingKV views) are recognised, with each cache's pool row, so that their
+    appends go out as one launch; separate rings, a shared row or a
+    non-contiguous view are not."""
+    compat = import_module("tm-opt_amd.compat")
+
+    class Ring:
+        def __init__(self, k, v):
+            self.k, self.v, self.n = k, v, 0
+
+    W, HK, D = 64, 2, 128
+    pk = torch.zeros((5, W, HK, D), dtype=torch.bfloat16)
+    pv = torch.zeros_like(pk)
+    got = compat._ring_pool([Ring(pk[s], pv[s]) for s in (3, 0, 2)])
+    assert got is not None
+    kpool, vpool, slots, per = got
+    assert slots == [3, 0, 2] and per == W // 16
+    assert kpool.shape == (5 * W // 16, 16, HK, D)
+    assert kpool.data_ptr() == pk.data_ptr() and vpool.data_ptr() == pv.data_ptr()
+    # page j of row s is pool page s * per + j
+    pk[2, 16:32] = 1
+    assert bool((kpool[2 * per + 1] == 1).all()) and not bool(kpool[2 * per].any())
+    sep = [Ring(torch.zeros((W, HK, D), dtype=torch.bfloat16),
+                torch.zeros((W, HK, D), dtype=torch.bfloat16)) for _ in range(2)]
+    assert compat._ring_pool(sep) is None
+    assert compat._ring_pool([Ring(pk[1], pv[1]), Ring(pk[1], pv[1])]) is None
+    assert compat._ring_pool([Ring(pk[1], pv[2])]) is None
+    odd = torch.zeros((3, W, HK, 2 * D), dtype=torch.bfloat16)[..., :D]
+    assert compat._ring_pool([Ring(odd[0], odd[1])]) is None

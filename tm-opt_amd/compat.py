@@ -134,6 +134,41 @@ def _to_device(rows, dev):
     return t.pin_memory().to(dev, non_blocking=True)
 
 
+def _ring_pool(caches):
+    """Rings that are rows of one SwaPool (kv.py:231-245: LayerKV hands
+    RingKV views of pool rows): (k_pool, v_pool, slots, pages_per_ring),
+    the pools as [rows * W / 16, 16, HK, D] page views of the whole pool
+    storage and each cache's pool row, so that their appends take one
+    launch; None when the rings are not such views."""
+    c0 = caches[0]
+    if not all(hasattr(c, "k") and hasattr(c, "v") for c in caches):
+        return None
+    W, HK, D = c0.k.shape
+    if W % PAGE:
+        return None
+    row = W * HK * D
+    out = []
+    for name in ("k", "v"):
+        x0 = getattr(c0, name)
+        st = x0.untyped_storage()
+        slots = []
+        for c in caches:
+            x = getattr(c, name)
+            if (x.shape != (W, HK, D) or not x.is_contiguous() or
+                    x.dtype != x0.dtype or x.device != x0.device or
+                    x.untyped_storage().data_ptr() != st.data_ptr() or
+                    x.storage_offset() % row):
+                return None
+            slots.append(x.storage_offset() // row)
+        nrow = st.nbytes() // (row * x0.element_size())
+        out.append((x0.as_strided((nrow * (W // PAGE), PAGE, HK, D),
+                                  (PAGE * HK * D, HK * D, D, 1), 0), slots))
+    (kpool, ks), (vpool, vs) = out
+    if ks != vs or len(set(ks)) != len(ks):
+        return None
+    return kpool, vpool, ks, W // PAGE
+
+
 def _append_rows(k, v, caches, lens):
     """The prefill's cache population (model.py:507-512:
     st.cache.append(kn[i, :lens[i]], vv[i, :lens[i]])) done natively: each
@@ -143,9 +178,10 @@ def _append_rows(k, v, caches, lens):
     allocated on the host as
     PagedKV.append does (kv.py:196-198), ring rows as RingKV.append keeps
     them (kv.py:89-103); cache.n advances. Page caches that share one pool
-    (GlobalPool rows) take one batched launch for all rows; rings and
-    caches with pools of their own one launch each. Returns the int32
-    block-table rows of page caches ([B, num_pages]) or None for rings."""
+    (GlobalPool rows) take one batched launch for all rows, and so do
+    rings that are rows of one SwaPool; other rings and caches with pools
+    of their own take one launch each. Returns the int32 block-table rows
+    of page caches ([B, num_pages]) or None for rings."""
     B = k.shape[0]
     dev = k.device
     n0 = [int(c.n) for c in caches]
@@ -162,21 +198,24 @@ def _append_rows(k, v, caches, lens):
             c.ensure_pages((n0[i] + T[i] - 1) // c.page_size)
     rows = None
     if paged:
-        if all(getattr(c, "table_dev_row", None) is not None for c in caches):
-            rows = [c.table_dev_row.to(torch.int32) for c in caches]
-            width = max(r.shape[0] for r in rows)
-            rows = torch.stack([torch.nn.functional.pad(
-                r, (0, width - r.shape[0]), value=-1) for r in rows])
-        else:                                    # PagedKV with host tables
-            width = max(len(c.table) for c in caches)
-            rows = _to_device([list(c.table) + [-1] * (width - len(c.table))
-                               for c in caches], dev)
+        # the host tables (PagedKV.table, which ensure_pages just extended;
+        # a pool's device mirror holds the same ids) in one staged copy
+        width = max(len(c.table) for c in caches)
+        rows = _to_device([list(c.table) + [-1] * (width - len(c.table))
+                           for c in caches], dev)
     shared = paged and all(c.kp is caches[0].kp and c.vp is caches[0].vp
                            for c in caches)
+    pooled = None if paged else _ring_pool(caches)
     if shared:
         c0 = caches[0]
         attn.kv_append_rows(k, v, lens_d, start, rows, c0.kp, c0.vp,
                             max_len=max(T))
+    elif pooled is not None:
+        kpool, vpool, slots, per = pooled
+        table = _to_device([[s * per + j for j in range(per)] for s in slots],
+                           dev)
+        attn.kv_append_rows(k, v, lens_d, start, table, kpool, vpool,
+                            max_len=max(T), table_wrap=per)
     else:
         for i, c in enumerate(caches):
             kt = k[i, :T[i]]                     # [T, HK, D] view
@@ -184,9 +223,7 @@ def _append_rows(k, v, caches, lens):
             cu = meta[2 * B + 2 * i:2 * B + 2 * i + 2]
             if hasattr(c, "kp"):
                 row = (rows[i:i + 1].contiguous() if rows is not None else
-                       _to_device([list(c.table)], dev)
-                       if getattr(c, "table_dev_row", None) is None else
-                       c.table_dev_row.to(torch.int32)[None])
+                       _to_device([list(c.table)], dev))
                 attn.kv_write_paged(kt, vt, row, start[i:i + 1], c.kp, c.vp,
                                     cu_seqlens=cu, max_seqlen=T[i])
             else:
@@ -221,9 +258,9 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
     cache objects (PagedKV- or RingKV-shaped, empty: a whole-prompt
     prefill) and live lengths (default T) whose population the engine does
     just before this call (model.py:507-512). The adapter then appends the
-    rows itself from the same in-place K/V, and a global layer's attention
-    reads its keys back from those pages. Rings (SWA) cannot hold a prompt
-    longer than the window, so their attention reads the K/V tensors."""
+    rows itself, in one launch, from the same in-place K/V; the attention
+    reads the K/V tensors in place either way (reading them back from the
+    pages just written measured slower)."""
     B, H, T, D = q.shape
     HK = k.shape[1]
     E = rel.shape[3]
@@ -262,25 +299,12 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
     cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=dev)
     w = 0 if window is None else int(window)
     kr, vr = _kv_rows(k), _kv_rows(v)            # [B, T, HK, D]
-    table = None
     if caches is not None:
         assert len(caches) == B
         assert all(int(c.n) == 0 for c in caches), \
             "caches must be empty (chunked prefill: prefill_chunk_state)"
         lens = [T] * B if lens is None else [int(x) for x in lens]
-        table = _append_rows(kr, vr, caches, lens)
-        if not (table is not None and window is None and
-                all(c.kp is caches[0].kp for c in caches)):
-            table = None
-    if table is not None:
-        # keys back from the pages just written: no packed copy of K/V
-        c0 = caches[0]
-        attn.prefill_varlen(qp, None, None, cu, 1.0 / D, window=w,
-                            max_seqlen=T, k_pool=c0.kp, v_pool=c0.vp,
-                            block_table=table.contiguous(), rel=relp,
-                            out=out.view(B * T, H, D), return_lse=False,
-                            reject=reject)
-        return out
+        _append_rows(kr, vr, caches, lens)
     attn.prefill_varlen(qp, kr, vr, cu, 1.0 / D, window=w, max_seqlen=T,
                         rel=relp, out=out.view(B * T, H, D),
                         return_lse=False, reject=reject)

@@ -22,7 +22,7 @@
  *   - Results are deterministic: fixed reduction order, no atomics.
  *
  * Supported shapes: D == 128, page_size == 16, HQ % HKV == 0 with
- * REP = HQ / HKV in {1, 2, 4, 8, 16} for decode and {4, 8} for prefill.
+ * REP = HQ / HKV in {1, 2, 4, 8, 16} for decode and {1, 2, 4, 8} for prefill.
  * Other shapes return TMOPT_EUNSUPPORTED.
  */
 #ifndef TMOPT_ATTN_H

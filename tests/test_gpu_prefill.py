@@ -2,7 +2,7 @@
 
 Tolerances: outputs max-abs 2e-2 / rtol 1e-2, LSE 1e-3.
 Covers ragged lengths around the 32-query / 64-key tile edges, causal and
-windowed masks, GQA 4 and 8, strided inputs, chunked prefill reading prior
+windowed masks, GQA 1, 2, 4 and 8, strided inputs, chunked prefill reading prior
 context from a shuffled paged cache, the fused relative bias (band shorter
 than the runs, so most key tiles carry none; packed and paged sources), the
 q = 0 closed form (LSE = ln(#visible keys)), determinism, config 4 at full
@@ -36,7 +36,7 @@ def _gpu(tm, case, dev, **kw):
 
 
 @pytest.mark.parametrize("window", [0, 1, 17, 64, 100])
-@pytest.mark.parametrize("hq,hkv", [(32, 4), (64, 16)])
+@pytest.mark.parametrize("hq,hkv", [(32, 4), (64, 16), (8, 8), (16, 8)])
 def test_ragged_lengths(tm, dev, window, hq, hkv):
     case = _wl().make_prefill("ragged", 21, lens=LENS, window=window, hq=hq,
                               hkv=hkv)
@@ -49,7 +49,8 @@ def test_ragged_lengths(tm, dev, window, hq, hkv):
 
 
 @pytest.mark.parametrize("hq,hkv", [(8, 1), (16, 2), (24, 3), (32, 4),
-                                    (64, 16)])
+                                    (64, 16), (4, 4), (6, 3), (16, 16),
+                                    (24, 12)])
 def test_every_row_written(tm, dev, hq, hkv):
     """The work-group -> (KV head, run, query block) schedule covers every
     row: 70 runs (more than one wave's worth of runs) of ragged lengths,
@@ -115,14 +116,15 @@ def test_output_rows_8_byte_aligned(tm, dev):
 
 
 @pytest.mark.parametrize("window", [0, 48])
-def test_paged_prior_context(tm, dev, window):
+@pytest.mark.parametrize("HQ,HKV", [(32, 4), (8, 8), (8, 4)])
+def test_paged_prior_context(tm, dev, window, HQ, HKV):
     """Chunked prefill: each run's keys = prior context + its own tokens,
     all in a shuffled page pool (written by the KV-write kernel)."""
     g = torch.Generator().manual_seed(17)
     wl = _wl()
     prior = [0, 16, 100, 37, 300]
     lens = [17, 64, 129, 1, 90]
-    S, HQ, HKV, D = len(lens), 32, 4, 128
+    S, D = len(lens), 128
     table, P = wl.paged_layout(lens, g, pool_factor=2, prior=prior)
     tot = [p + t for p, t in zip(prior, lens)]
     kp = torch.full((P, 16, HKV, D), float("nan"), dtype=torch.bfloat16)
@@ -149,8 +151,8 @@ def test_paged_prior_context(tm, dev, window):
                                  k_pool=kp.to(dev), v_pool=vp.to(dev),
                                  block_table=table.to(dev))
     torch.cuda.synchronize()
-    assert_out_close(out, ref_o, f"paged w={window}")
-    assert_lse_close(lse, ref_l, f"paged w={window}")
+    assert_out_close(out, ref_o, f"paged w={window} {HQ}/{HKV}")
+    assert_lse_close(lse, ref_l, f"paged w={window} {HQ}/{HKV}")
 
 
 def test_zero_query_closed_form(tm, dev):
@@ -237,7 +239,7 @@ def test_one_long_run_sampled_rows(tm, dev):
 
 
 @pytest.mark.parametrize("E,window", [(95, 0), (1, 0), (80, 256), (300, 64)])
-@pytest.mark.parametrize("hq,hkv", [(32, 4), (64, 16)])
+@pytest.mark.parametrize("hq,hkv", [(32, 4), (64, 16), (8, 8), (8, 4)])
 def test_bias_band_shorter_than_runs(tm, dev, E, window, hq, hkv):
     """Fused bias rel[t, h, dist] inside 0 <= dist < E: with E well below
     the run lengths most key tiles lie wholly outside the band and skip the

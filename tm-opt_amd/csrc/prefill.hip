@@ -1112,8 +1112,9 @@ extern "C" int tmopt_attn_prefill_varlen(
   TMOPT_REQUIRE(HKV > 0 && HQ > 0 && HQ % HKV == 0 && HKV <= 65535,
                 TMOPT_EINVAL, "prefill: HQ=%d HKV=%d", HQ, HKV);
   const int rep = HQ / HKV;
-  TMOPT_REQUIRE(rep == 4 || rep == 8, TMOPT_EUNSUPPORTED,
-                "prefill: HQ/HKV=%d not in {4, 8}", rep);
+  TMOPT_REQUIRE(rep == 1 || rep == 2 || rep == 4 || rep == 8,
+                TMOPT_EUNSUPPORTED, "prefill: HQ/HKV=%d not in {1, 2, 4, 8}",
+                rep);
   TMOPT_REQUIRE(window >= 0, TMOPT_EINVAL, "prefill: window=%d", window);
   TMOPT_REQUIRE(scale > 0.0f, TMOPT_EINVAL, "prefill: scale must be > 0");
   TMOPT_REQUIRE(rel == nullptr || rel_extent > 0, TMOPT_EINVAL,
@@ -1261,7 +1262,11 @@ extern "C" int tmopt_attn_prefill_varlen(
   hipStream_t st = (hipStream_t)stream;
   if (rep == 8)
     launch<8>(a, src, num_seqs, max_seqlen_q, st);
-  else
+  else if (rep == 4)
     launch<4>(a, src, num_seqs, max_seqlen_q, st);
+  else if (rep == 2)
+    launch<2>(a, src, num_seqs, max_seqlen_q, st);
+  else
+    launch<1>(a, src, num_seqs, max_seqlen_q, st);
   return check_launch("prefill");
 }

@@ -288,12 +288,22 @@ def test_attn_prefill_fused_model_shape(tm, dev, kind, with_caches):
         caches = [PagedCache(kp, vp, free, torch.zeros(
             T // 16 + 8, dtype=torch.int64, device=dev)) for _ in range(B)]
     elif with_caches:
-        caches = [RingCache(torch.zeros((E, hk, D), dtype=bf, device=dev),
-                            torch.zeros((E, hk, D), dtype=bf, device=dev))
-                  for _ in range(B)]
+        # rows of one SwaPool in a permuted slot order (the engine's pooled
+        # rings): one append launch for the six rows, T > W, so only each
+        # row's last W tokens survive (RingKV's drop rule)
+        pk = torch.zeros((B + 1, E, hk, D), dtype=bf, device=dev)
+        pv = torch.zeros_like(pk)
+        slots = torch.randperm(B + 1, generator=g)[:B].tolist()
+        caches = [RingCache(pk[s], pv[s]) for s in slots]
     out = tm.attn_prefill_fused(q, k, v, rel, ar, ar, window, caches=caches)
     torch.cuda.synchronize()
     assert out.shape == (B, T, hq, D)
+    if with_caches and kind == "swa":
+        pos = torch.arange(T - E, T)
+        for b, s in enumerate(slots):
+            for x, pool in ((k, pk), (v, pv)):
+                want = x[b].transpose(0, 1)[T - E:]           # [E, hk, D]
+                assert torch.equal(pool[s][pos % E], want), (b, s)
     rows = _edge_rows(T, 24, g)
     ref = attn_ref.prefill_reference_semantics(
         q.cpu(), k.cpu(), v.cpu(), rel.cpu(), ar.cpu(), window, rows=rows)

@@ -56,6 +56,7 @@ constexpr int kRowB = 256;                // K / V tile row in LDS (one key)
 constexpr int kTileB = kBN * kRowB;       // 16384
 constexpr int kStage = 2 * kTileB;        // K tile then V tile
 constexpr int kNStage = 4;                // 128 KB of LDS per work-group
+constexpr int kBiasB = 32 * 128;          // fused bias: 32 window rows per wave
 constexpr int kPage = 16;                 // paged source: tokens per page
 constexpr float kLazy = 8.0f;             // lazy-rescale threshold (log2)
 constexpr int kRing = 4;                  // MFMA-phase fragment ring
@@ -88,6 +89,16 @@ __device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
 __device__ __forceinline__ void dma(i32x4 rsrc, uint32_t lds, int voff) {
   asm volatile(
       "s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(lds), "v"(voff), "s"(rsrc)
+      : "memory", "m0");
+}
+
+// 4 bytes per lane into LDS: lane l of the wave writes bytes lds + 4 l ..
+// +3 (the fused bias's window rows; the same rules as dma())
+__device__ __forceinline__ void dma32(i32x4 rsrc, uint32_t lds, uint32_t voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dword %1, %2, 0 offen lds"
       :
       : "s"(lds), "v"(voff), "s"(rsrc)
       : "memory", "m0");
@@ -569,21 +580,65 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   [[maybe_unused]] const int rrow_b =
       REL ? rel_mis + l32 * (int)(a.r_st * 2) : 0;
 
-  // The fused bias of a key tile, loaded one softmax ahead (bias_issue)
-  // and applied in the softmax (bias_apply). The lane's keys come in runs
-  // of four (key0 .. key0+3, dist d0 .. d0-3), whose four bf16 values are
-  // adjacent in the row: the three dwords from the one holding rel[d0-3],
-  // realigned by 0 or 2 bytes. The range check is per dword and the
+  // The fused bias of a key tile: the lane's keys come in runs of four
+  // (key0 .. key0+3, dist d0 .. d0-3), whose four bf16 values are adjacent
+  // in the row: the three dwords from the one holding rel[d0-3], realigned
+  // by the lane's byte shift rel_sh.
+  // The first tile of an item loads its runs straight into registers (rb,
+  // 8 loads of 12 bytes issued before the first softmax). Every later tile
+  // goes through LDS: one softmax ahead, each wave copies the 64-key window
+  // of each of its 32 rows (dists q-kt-63 .. q-kt, 32 dwords from the one
+  // holding rel[q-kt-63]; a row whose values start mid-dword takes the 32
+  // dwords from q-kt-64 and so lacks rel[q-kt]) into its 4 KB of LDS, two
+  // rows per 4-byte-per-lane DMA, and reads its runs back from there: 16
+  // DMAs that touch the rows' own lines instead of 8 loads that each touch
+  // 32 rows. Rows 2m and 2m+1 take the 256 bytes of DMA m, with dword j of
+  // the window in slot j ^ 2m: the 32 rows' reads of one dword pair then
+  // fall on 32 distinct bank pairs (plain rows, 128 bytes apart, would put
+  // all 32 on two). A lane reads the first two dwords of each run (one
+  // 8-byte read); the third is the first of another lane's run on the same
+  // row (the low half's comes from the high half's previous run, the high
+  // half's from the low half's same run), swapped across the lane halves.
+  // The value a mid-dword row lacks, the third dword of the low half's
+  // first run, is the first dword of the previous tile's window (`carry`,
+  // the high half's last run). The range check is per dword and the
   // resource ends at a dword boundary, so every value of the rows arrives;
-  // the whole offset goes in the lane register, where the check sees it.
-  // Every call issues exactly 8 loads (a tile outside the band or past the
-  // run reads nothing), so the wave's load counts stay fixed: the waits
-  // at the end of the odd slots count them exactly.
+  // dwords before a row or past the run read as zeros or as a neighbouring
+  // row's values, which lie outside the band and are dropped.
   typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
   [[maybe_unused]] u32x3 rb[8];
+  [[maybe_unused]] uint32_t carry = 0;
+  [[maybe_unused]] const uint32_t bb =
+      lds0 + kNStage * kStage + (uint32_t)w * kBiasB;
+  [[maybe_unused]] const i32x4 rrel_s = make_rsrc(
+      rel_first - rel_mis,
+      rel_nrow > 0 ? (uint32_t)(((((int64_t)(rel_nrow - 1) * a.r_st +
+                                   a.rel_extent) * 2) + rel_mis + 3) & ~3)
+                   : 0u);
+  // DMA i (rows 2i and 2i+1 of the wave): lane l fills slot l & 31 of row
+  // 2i + (l >> 5), i.e. dword (l & 31) ^ 2i of its window; its byte offset
+  // is dma_b + i * dma_s + ((4 (l & 31)) ^ 8i) - 2 kt
+  [[maybe_unused]] uint32_t dma_b = 0, dma_s = 0, dma_c = 0;
+  // LDS byte address of the lane's row with its swizzle and lane half
+  // folded in: dword j ^ 2 h2 of the window sits at bias_a ^ 4j
+  [[maybe_unused]] uint32_t bias_a = 0;
+  if constexpr (REL) {
+    const int hl = lane >> 5;
+    const int x0 = rel_mis + hl * (int)(a.r_st * 2) +
+                   2 * (prior + rel_row0 + hl - 63);
+    dma_b = (uint32_t)(x0 - (x0 & 2));
+    dma_s = (uint32_t)(4 * a.r_st + 4);
+    dma_c = 4u * (uint32_t)(lane & 31);
+    bias_a = (bb + 256u * (uint32_t)(l32 >> 1) + 128u * (uint32_t)(l32 & 1)) |
+             (8u * (uint32_t)((l32 >> 1) ^ h2));
+  }
+  // the first tile's runs, into registers
   [[maybe_unused]] auto bias_issue = [&](int kt) {
     if constexpr (REL) {
-      const bool band_tile = kt < k_hi && pos_lo - (kt + kBN - 1) < a.rel_extent;
+      // (also when only the next tile is in the band: its first runs need
+      // this window's first dword)
+      const bool band_tile =
+          kt < k_hi && pos_lo - (kt + 2 * kBN - 1) < a.rel_extent;
       // byte offset of rel[d0 - 3] for kb = g = 0, opaque to the compiler
       // so that the eight offsets are derived from it here rather than
       // hoisted out of the key loop as eight live registers
@@ -596,15 +651,46 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
           const int b4 = (base - 64 * kb - 16 * g) & ~3;
           // before the first row (row 0 near dist 0): from the row start,
           // shifted back into place by bias_apply
-          int off = band_tile ? (b4 < 0 ? 0 : b4) : 0x7ffffff0;
+          int off = band_tile ? (b4 < 0 ? 0 : b4) : kOob;
           asm volatile("" : "+v"(off));
           rb[4 * kb + g] = __builtin_bit_cast(
               u32x3, __builtin_amdgcn_raw_buffer_load_b96(rrel, off, 0, 0));
         }
     }
   };
-  // the scores move to the log2 domain: s*scale*log2e + rel*log2e,
-  // rel[q, h, dist] for 0 <= dist < E, zero outside
+  // a later tile's windows, into LDS (always 16 DMAs; a tile neither in
+  // the band nor just before it, or past the run, fetches nothing)
+  [[maybe_unused]] auto bias_dma = [&](int kt) {
+    if constexpr (REL) {
+      const bool live =
+          kt < k_hi && pos_lo - (kt + 2 * kBN - 1) < a.rel_extent;
+      uint32_t b = live ? dma_b - 2u * (uint32_t)kt : (uint32_t)kOob;
+      asm volatile("" : "+v"(b));
+#pragma unroll
+      for (int i = 0; i < 16; ++i)
+        dma32(rrel_s, bb + 256 * i, b + i * dma_s + (dma_c ^ (8u * i)));
+    }
+  };
+  // the runs of the tile whose windows are in LDS
+  [[maybe_unused]] auto bias_read = [&](u32x3 (&x)[8]) {
+    if constexpr (REL) {
+      // run r = 4 kb + g: dword 30 - 4 r - 2 h2 of the row's window holds
+      // rel[d0-3]
+      u32x2 lo[8];
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+        lo[r] = lds_ld64(bias_a ^ (4u * (uint32_t)(30 - 4 * r)));
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        // the low half takes the high half's lo[r-1][0] (dword 32 - 4 r,
+        // for r = 0 the carry), the high half the low half's lo[r][0]
+        const auto sw = __builtin_amdgcn_permlane32_swap(
+            r == 0 ? carry : lo[r - 1][0], lo[r][0], false, false);
+        x[r] = u32x3{lo[r][0], lo[r][1], (uint32_t)(h2 ? sw[0] : sw[1])};
+      }
+      carry = lo[7][0];
+    }
+  };
   // Byte shift that realigns a lane's runs: the same on every tile (tile
   // starts are multiples of 64 keys, so only the row's parity matters).
   [[maybe_unused]] const uint32_t rel_sh =
@@ -614,9 +700,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // FAST (a whole tile with every dist in [0, E) for every query: no mask,
   // no band test, every run starts inside its row) costs two byte-aligns
   // per run and two instructions per score; the checked path handles the
-  // tiles at the diagonal, the run ends and the band edge.
-  [[maybe_unused]] auto bias_apply = [&](f32x16 (&s)[2], int kt, auto fast_c) {
+  // tiles at the diagonal, the run ends and the band edge. VMEM: the runs
+  // of the first tile, whose loads start at the row when the run begins
+  // before it.
+  [[maybe_unused]] auto bias_apply = [&](f32x16 (&s)[2], int kt,
+                                         const u32x3 (&x)[8], auto fast_c,
+                                         auto vmem_c) {
     constexpr bool fast = decltype(fast_c)::value;
+    constexpr bool vmem = decltype(vmem_c)::value;
     if constexpr (REL) {
       // dist of the lane's first key for kb = g = 0 (opaque, as above)
       int dq = qpos - kt - 4 * h2;
@@ -626,10 +717,10 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d0 = dq - 32 * kb - 8 * g;
-          const uint32_t x0 = rb[4 * kb + g][0], x1 = rb[4 * kb + g][1],
-                         x2 = rb[4 * kb + g][2];
+          const uint32_t x0 = x[4 * kb + g][0], x1 = x[4 * kb + g][1],
+                         x2 = x[4 * kb + g][2];
           uint32_t w0, w1;
-          if constexpr (fast) {
+          if constexpr (fast || !vmem) {
             w0 = __builtin_amdgcn_alignbyte(x1, x0, rel_sh);
             w1 = __builtin_amdgcn_alignbyte(x2, x1, rel_sh);
           } else {
@@ -755,24 +846,45 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 
   // softmax of scores `s` of the tile at kt (masking when needed): P^T
   // fragments, running max / sum update, O^T rescale when the max moved.
-  // `hook` runs once the tile's bias loads have arrived (the fused-bias
-  // loops issue their tile DMA there, past the compiler's wait for them).
-  auto softmax_phase = [&](f32x16 (&s)[2], int kt, bool first, auto&& hook) {
+  // `hook` runs once the tile's bias is in registers (the fused-bias loops
+  // issue the next tile's bias DMA and their tile DMA there); with the
+  // fused bias, `wv` DMAs issued after this tile's bias windows may still
+  // be in flight.
+  auto softmax_phase = [&](f32x16 (&s)[2], int kt, bool first, int wv,
+                           auto&& hook) {
     // the bias band: some pair of the tile has dist = q - k < E (the
     // smallest dist is pos_lo - (kt + 63))
     const bool with_bias = REL && pos_lo - (kt + kBN - 1) < a.rel_extent;
     const bool full = full_tile(kt);
     if constexpr (REL) {
-      // every tile waits for its bias loads here, used or not, so that no
-      // load into a dead register is left in flight to be waited for
-      // later (past the tile DMA issued by `hook` below)
+      constexpr std::true_type kT{};
+      constexpr std::false_type kF{};
+      const bool fast = full && pos_hi - kt < a.rel_extent;
+      if (first) {
+        // the first tile waits for its loads here, used or not, so that no
+        // load into a dead register is left in flight to be waited for
+        // later (past the DMAs issued by `hook` below)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(rb[i]));
-      if (with_bias) {
-        if (full && pos_hi - kt < a.rel_extent)
-          bias_apply(s, kt, std::true_type{});
-        else
-          bias_apply(s, kt, std::false_type{});
+        for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(rb[i]));
+        carry = rb[7][0];
+        if (with_bias) {
+          if (fast) bias_apply(s, kt, rb, kT, kT);
+          else bias_apply(s, kt, rb, kF, kT);
+        }
+      } else {
+        if (wv == 0) wait_vm<0>();
+        else wait_vm<4>();
+        asm volatile("" ::: "memory");   // the LDS reads stay below the wait
+        if (with_bias) {
+          u32x3 x[8];
+          bias_read(x);
+          if (fast) bias_apply(s, kt, x, kT, kF);
+          else bias_apply(s, kt, x, kF, kF);
+        } else {
+          carry = lds_ld64(bias_a ^ 8u)[0];
+        }
+        // read before the next DMA into the same LDS goes out
+        asm volatile("" : "+v"(carry));
       }
     }
     hook();
@@ -900,19 +1012,18 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   if (ntiles > 2) issue_tile(2, 2);
   // End of every odd slot: this wave's part of tile t+2 must be in LDS
   // before the barrier that publishes it. Loads issued after that tile's
-  // may still fly: the DMA of tile t+3 and, with the fused bias, the bias
-  // loads of the tile after the next softmax (`bias` of them).
-  auto odd_end = [&](int n_dma, int bias) {
-    const int n = n_dma + bias;
-    if (n == 12) wait_vm<12>();
-    else if (n == 8) wait_vm<8>();
+  // may still fly: the DMA of tile t+3 and, with the fused bias, the 16
+  // window DMAs of the tile after the next softmax (n in all).
+  auto odd_end = [&](int n) {
+    if (n == 20) wait_vm<20>();
     else if (n == 4) wait_vm<4>();
     else wait_vm<0>();
     __syncthreads();
   };
-  constexpr int NB = REL ? 8 : 0;   // bias loads per tile
+  constexpr int NB = REL ? 16 : 0;   // bias DMAs per tile
   // With the fused bias a wave issues its tile DMA inside its softmax, right
-  // after the wait for that tile's bias loads, and not before: group 0 in
+  // after it has read that tile's bias windows and sent the next tile's
+  // window DMAs, and not before: group 0 in
   // slot 2t+1, group 1 in slot 2t (tile t+3's stage is free from slot 2t
   // on; the DMA then lands over the next one to two slots).
   // The first and last tiles are peeled off the loops, so that the loops
@@ -933,48 +1044,52 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   if (grp_id == 0) {
     scores(0, sc);
     bias_issue(k_lo);
-    softmax_phase(sc, k_lo, true, none);
-    bias_issue(k_lo + kBN);
+    softmax_phase(sc, k_lo, true, 0, [&] { bias_dma(k_lo + kBN); });
     for (int t = 0; t + 1 < ntiles; ++t) {
       if constexpr (!REL) issue_tile(t + 3, (t + 3) & 3, t + 3 < ntiles);
       mfma_phase(t, kWithS);
       mid_sync();
-      softmax_phase(sc, k_lo + (t + 1) * kBN, false, [&] {
-        if constexpr (REL) issue_tile(t + 3, (t + 3) & 3, t + 3 < ntiles);
+      // tile t+1's bias windows went out before tile t+2's DMA (t > 0)
+      softmax_phase(sc, k_lo + (t + 1) * kBN, false, t == 0 ? 0 : 4, [&] {
+        if constexpr (REL) {
+          bias_dma(k_lo + (t + 2) * kBN);
+          issue_tile(t + 3, (t + 3) & 3, t + 3 < ntiles);
+        }
       });
-      bias_issue(k_lo + (t + 2) * kBN);
-      odd_end(4, NB);
+      odd_end(NB + 4);
     }
     mfma_phase(ntiles - 1, kNoS);
     mid_sync();
-    odd_end(0, 0);   // everything, before the output goes through LDS
+    odd_end(0);   // everything, before the output goes through LDS
   } else {
     if constexpr (!REL) issue_tile(3, 3, 3 < ntiles);
     scores(0, sc);
     bias_issue(k_lo);
-    softmax_phase(sc, k_lo, true, [&] {
-      if constexpr (REL) issue_tile(3, 3, 3 < ntiles);
+    softmax_phase(sc, k_lo, true, 0, [&] {
+      if constexpr (REL) {
+        bias_dma(k_lo + kBN);
+        issue_tile(3, 3, 3 < ntiles);
+      }
     });
-    bias_issue(k_lo + kBN);
     mid_sync();
     if (ntiles > 1) mfma_phase(0, kWithS);
     else mfma_phase(0, kNoS);
-    odd_end(ntiles > 1 ? 4 : 0, NB);
+    odd_end(ntiles > 1 ? NB + 4 : 0);
     for (int t = 1; t + 1 < ntiles; ++t) {
-      softmax_phase(sc, k_lo + t * kBN, false,
-                    [&] { issue_tile(t + 3, (t + 3) & 3, t + 3 < ntiles); });
-      bias_issue(k_lo + (t + 1) * kBN);
+      softmax_phase(sc, k_lo + t * kBN, false, 4, [&] {
+        bias_dma(k_lo + (t + 1) * kBN);
+        issue_tile(t + 3, (t + 3) & 3, t + 3 < ntiles);
+      });
       mid_sync();
       mfma_phase(t, kWithS);
-      odd_end(4, NB);
+      odd_end(NB + 4);
     }
     if (ntiles > 1) {
       const int t = ntiles - 1;
-      softmax_phase(sc, k_lo + t * kBN, false, none);
-      bias_issue(k_lo + (t + 1) * kBN);
+      softmax_phase(sc, k_lo + t * kBN, false, 4, none);
       mid_sync();
       mfma_phase(t, kNoS);
-      odd_end(0, NB);   // the tile loads, before the output goes through LDS
+      odd_end(0);   // the tile loads, before the output goes through LDS
     }
   }
   }  // !rejected
@@ -1055,7 +1170,7 @@ void launch(PrefillArgs a, int src, int S, int max_seqlen, hipStream_t st) {
   int64_t n = a.HKV * items;
   if (a.HKV <= 8 && 8 % a.HKV == 0) n = 8 * ((items + 8 / a.HKV - 1) / (8 / a.HKV));
   const dim3 grid((unsigned)n);
-  const size_t lds = kNStage * kStage;
+  const size_t lds = kNStage * kStage + (a.rel ? 8 * kBiasB : 0);
   if (a.rel)
     launch_src<REP, true>(a, src, grid, lds, st);
   else

@@ -523,10 +523,13 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   };
 
   // S^T = K.Q^T for the tile in `stage` (keys on M, queries on N)
+  // (with the fused bias, s already holds the tile's bias / scale)
   auto scores = [&](int stage, f32x16 (&s)[2]) {
     const uint32_t kt_b = lds0 + stage * kStage;
-    s[0] = f32x16{};
-    s[1] = f32x16{};
+    if constexpr (!REL) {
+      s[0] = f32x16{};
+      s[1] = f32x16{};
+    }
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
@@ -580,13 +583,15 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   [[maybe_unused]] const int rrow_b =
       REL ? rel_mis + l32 * (int)(a.r_st * 2) : 0;
 
-  // The fused bias of a key tile: the lane's keys come in runs of four
+  // The fused bias of a key tile enters as the initial value of its score
+  // accumulators, bias / scale (zero outside the band), so that the tile's
+  // softmax is the plain one. The lane's keys come in runs of four
   // (key0 .. key0+3, dist d0 .. d0-3), whose four bf16 values are adjacent
   // in the row: the three dwords from the one holding rel[d0-3], realigned
   // by the lane's byte shift rel_sh.
   // The first tile of an item loads its runs straight into registers (rb,
-  // 8 loads of 12 bytes issued before the first softmax). Every later tile
-  // goes through LDS: one softmax ahead, each wave copies the 64-key window
+  // 8 loads of 12 bytes before its scores). Every later tile goes through
+  // LDS: one MFMA phase ahead, each wave copies the 64-key window
   // of each of its 32 rows (dists q-kt-63 .. q-kt, 32 dwords from the one
   // holding rel[q-kt-63]; a row whose values start mid-dword takes the 32
   // dwords from q-kt-64 and so lacks rel[q-kt]) into its 4 KB of LDS, two
@@ -660,15 +665,20 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   };
   // a later tile's windows, into LDS (always 16 DMAs; a tile neither in
   // the band nor just before it, or past the run, fetches nothing)
+  [[maybe_unused]] auto bias_dma_base = [&](int kt) {
+    const bool live = kt < k_hi && pos_lo - (kt + 2 * kBN - 1) < a.rel_extent;
+    uint32_t b = live ? dma_b - 2u * (uint32_t)kt : (uint32_t)kOob;
+    asm volatile("" : "+v"(b));
+    return b;
+  };
+  [[maybe_unused]] auto bias_dma_one = [&](uint32_t b, int i) {
+    dma32(rrel_s, bb + 256 * i, b + i * dma_s + (dma_c ^ (8u * i)));
+  };
   [[maybe_unused]] auto bias_dma = [&](int kt) {
     if constexpr (REL) {
-      const bool live =
-          kt < k_hi && pos_lo - (kt + 2 * kBN - 1) < a.rel_extent;
-      uint32_t b = live ? dma_b - 2u * (uint32_t)kt : (uint32_t)kOob;
-      asm volatile("" : "+v"(b));
+      const uint32_t b = bias_dma_base(kt);
 #pragma unroll
-      for (int i = 0; i < 16; ++i)
-        dma32(rrel_s, bb + 256 * i, b + i * dma_s + (dma_c ^ (8u * i)));
+      for (int i = 0; i < 16; ++i) bias_dma_one(b, i);
     }
   };
   // the runs of the tile whose windows are in LDS
@@ -695,17 +705,17 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // starts are multiples of 64 keys, so only the row's parity matters).
   [[maybe_unused]] const uint32_t rel_sh =
       REL ? (uint32_t)((rrow_b + 2 * (qpos - 3)) & 3) : 0u;
-  // The scores of a bias tile move to the natural-log domain with the bias
-  // added: s*scale + rel[q, h, dist] for 0 <= dist < E, zero outside.
-  // FAST (a whole tile with every dist in [0, E) for every query: no mask,
-  // no band test, every run starts inside its row) costs two byte-aligns
-  // per run and two instructions per score; the checked path handles the
-  // tiles at the diagonal, the run ends and the band edge. VMEM: the runs
-  // of the first tile, whose loads start at the row when the run begins
-  // before it.
-  [[maybe_unused]] auto bias_apply = [&](f32x16 (&s)[2], int kt,
-                                         const u32x3 (&x)[8], auto fast_c,
-                                         auto vmem_c) {
+  // The score accumulators of a bias tile start at rel[q, h, dist] / scale
+  // for 0 <= dist < E, zero outside (the softmax multiplies by scale).
+  // FAST (a whole tile with every dist in [0, E) for every query: no band
+  // test, every run starts inside its row) costs two byte-aligns per run
+  // and two instructions per score; the checked path handles the tiles at
+  // the diagonal, the run ends and the band edge. VMEM: the runs of the
+  // first tile, whose loads start at the row when the run begins before it.
+  [[maybe_unused]] const float inv_scale = REL ? 1.0f / a.scale : 0.0f;
+  [[maybe_unused]] auto bias_init = [&](f32x16 (&s)[2], int kt,
+                                        const u32x3 (&x)[8], auto fast_c,
+                                        auto vmem_c) {
     constexpr bool fast = decltype(fast_c)::value;
     constexpr bool vmem = decltype(vmem_c)::value;
     if constexpr (REL) {
@@ -747,7 +757,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
               const bool band = qok && dist >= 0 && dist < a.rel_extent;
               bias = band ? bias : 0.0f;
             }
-            s[kb][4 * g + i] = __builtin_fmaf(s[kb][4 * g + i], a.scale, bias);
+            s[kb][4 * g + i] = bias * inv_scale;
           }
         }
     }
@@ -844,52 +854,54 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   f32x16 sc[2];        // scores of the tile after the one being multiplied
   bf16x8 pf[2][2];     // probabilities of the tile being multiplied
 
-  // softmax of scores `s` of the tile at kt (masking when needed): P^T
-  // fragments, running max / sum update, O^T rescale when the max moved.
-  // `hook` runs once the tile's bias is in registers (the fused-bias loops
-  // issue the next tile's bias DMA and their tile DMA there); with the
-  // fused bias, `wv` DMAs issued after this tile's bias windows may still
-  // be in flight.
-  auto softmax_phase = [&](f32x16 (&s)[2], int kt, bool first, int wv,
-                           auto&& hook) {
-    // the bias band: some pair of the tile has dist = q - k < E (the
-    // smallest dist is pos_lo - (kt + 63))
-    const bool with_bias = REL && pos_lo - (kt + kBN - 1) < a.rel_extent;
-    const bool full = full_tile(kt);
+  // The bias of the tile at kt into its score accumulators: the first tile
+  // from its loads (FIRST), a later one from its windows in LDS, whose DMAs
+  // were followed by 4 tile DMAs at most; the windows are read before the
+  // next tile's DMAs into the same LDS go out (the carry is the last read).
+  [[maybe_unused]] auto bias_tile = [&](f32x16 (&s)[2], int kt, auto first_c) {
     if constexpr (REL) {
+      constexpr bool first = decltype(first_c)::value;
       constexpr std::true_type kT{};
       constexpr std::false_type kF{};
-      const bool fast = full && pos_hi - kt < a.rel_extent;
-      if (first) {
-        // the first tile waits for its loads here, used or not, so that no
-        // load into a dead register is left in flight to be waited for
-        // later (past the DMAs issued by `hook` below)
+      const bool with_bias = pos_lo - (kt + kBN - 1) < a.rel_extent;
+      const bool fast = full_tile(kt) && pos_hi - kt < a.rel_extent;
+      if constexpr (first) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(rb[i]));
         carry = rb[7][0];
         if (with_bias) {
-          if (fast) bias_apply(s, kt, rb, kT, kT);
-          else bias_apply(s, kt, rb, kF, kT);
+          if (fast) bias_init(s, kt, rb, kT, kT);
+          else bias_init(s, kt, rb, kF, kT);
+        } else {
+          s[0] = f32x16{};
+          s[1] = f32x16{};
         }
       } else {
-        if (wv == 0) wait_vm<0>();
-        else wait_vm<4>();
+        wait_vm<4>();
         asm volatile("" ::: "memory");   // the LDS reads stay below the wait
         if (with_bias) {
           u32x3 x[8];
           bias_read(x);
-          if (fast) bias_apply(s, kt, x, kT, kF);
-          else bias_apply(s, kt, x, kF, kF);
+          if (fast) bias_init(s, kt, x, kT, kF);
+          else bias_init(s, kt, x, kF, kF);
         } else {
+          s[0] = f32x16{};
+          s[1] = f32x16{};
           carry = lds_ld64(bias_a ^ 8u)[0];
         }
-        // read before the next DMA into the same LDS goes out
         asm volatile("" : "+v"(carry));
       }
     }
+  };
+
+  // softmax of scores `s` of the tile at kt (masking when needed): P^T
+  // fragments, running max / sum update, O^T rescale when the max moved.
+  // `hook` runs first (group 1 issues its tile DMA there).
+  auto softmax_phase = [&](f32x16 (&s)[2], int kt, bool first, auto&& hook) {
+    const bool full = full_tile(kt);
     hook();
     if (!full) mask_tile(s, kt);
-    const float sl2 = with_bias ? kLog2e : a.scale_log2;
+    const float sl2 = a.scale_log2;
     float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -924,14 +936,25 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // MFMA phase of tile t: O^T += V^T.P^T for tile t (four accumulators in
   // turn) interleaved with the scores of tile t+1 (two accumulators), the
   // V^T and K fragments read kRing - 1 MFMAs ahead (3: measured ~1% over 4
-  // and 5 ahead on 4K-16K runs; 2 with the fused bias)
-  auto mfma_phase = [&](int t, auto with_s_c) {
+  // and 5 ahead on 4K-16K runs; 2 with the fused bias). With the fused
+  // bias the phase first puts tile t+1's bias into its score accumulators,
+  // then sends the 16 window DMAs of tile t+2 two per MFMA step over the
+  // first eight steps (beside the MFMAs instead of in a row before them:
+  // ~3% on the adapters' shapes). (Inlined: as a call, its captures would
+  // travel through memory and the DMAs' scalar operands into vector
+  // registers.)
+  auto mfma_phase = [&](int t, auto with_s_c) __attribute__((always_inline)) {
     // (with_s as a type: one straight-line copy per case, no branch between
     // the MFMAs)
     constexpr bool with_s = decltype(with_s_c)::value;
     // the SIMD's issue port goes to this wave's MFMAs first; the softmax
     // wave fills the slots in between (measured ~2% over equal priority)
     __builtin_amdgcn_s_setprio(1);
+    [[maybe_unused]] uint32_t b2 = 0;
+    if constexpr (with_s && REL) {
+      bias_tile(sc, k_lo + (t + 1) * kBN, std::false_type{});
+      b2 = bias_dma_base(k_lo + (t + 2) * kBN);
+    }
     const uint32_t vt_b = lds0 + (t & 3) * kStage + kTileB;
     const uint32_t kt_b = lds0 + ((t + 1) & 3) * kStage;
     auto vf_n = [&](int n) {
@@ -939,9 +962,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
       return vfrag(vt_b, db, kb, kk);
     };
     auto kf_n = [&](int n) { return kfrag(kt_b, n & 1, n >> 1); };
-    // fragments read R - 1 MFMAs ahead; one fewer with the fused bias, whose
-    // prefetched values need the registers (the fourth slot made the bias
-    // build spill: 2-3% slower on the adapters' shapes)
+    // fragments read R - 1 MFMAs ahead; one fewer with the fused bias (a
+    // fourth slot measured no faster there)
     constexpr int R = REL ? kRing - 1 : kRing;
     bf16x8 vf[R], kf[R];
 #pragma unroll
@@ -959,7 +981,14 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
       if (with_s) {
         const int skb = n & 1, skk = n >> 1;
         sc[skb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-            kf[n % R], qf[skk], n < 2 ? f32x16{} : sc[skb], 0, 0, 0);
+            kf[n % R], qf[skk], (!REL && n < 2) ? f32x16{} : sc[skb], 0, 0,
+            0);
+      }
+      if constexpr (with_s && REL) {
+        if (n < 8) {
+          bias_dma_one(b2, 2 * n);
+          bias_dma_one(b2, 2 * n + 1);
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1020,12 +1049,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     else wait_vm<0>();
     __syncthreads();
   };
-  constexpr int NB = REL ? 16 : 0;   // bias DMAs per tile
-  // With the fused bias a wave issues its tile DMA inside its softmax, right
-  // after it has read that tile's bias windows and sent the next tile's
-  // window DMAs, and not before: group 0 in
-  // slot 2t+1, group 1 in slot 2t (tile t+3's stage is free from slot 2t
-  // on; the DMA then lands over the next one to two slots).
+  constexpr int NB = REL ? 16 : 0;   // bias window DMAs per tile
+  // Tile t+3's DMA goes out in slot 2t, where its stage is free: group 0
+  // before its MFMA phase, group 1 at the start of its softmax. With the
+  // fused bias, the MFMA phase's wait for its windows (4 DMAs at most
+  // after them) also covers tile t+2.
   // The first and last tiles are peeled off the loops, so that the loops
   // hold one variant of the MFMA phase: O^T then keeps one set of
   // registers across iterations (variants merged inside the loop made the
@@ -1033,61 +1061,46 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   constexpr std::true_type kWithS{};
   constexpr std::false_type kNoS{};
   auto none = [] {};
-  // The barrier between the two phases of a slot only keeps the groups in
-  // step: a tile is published, and its stage freed, at the odd slots'
-  // barriers alone. The plain build runs without it (~2% faster on C4 and
-  // 4x8192, outputs bitwise equal); the bias build keeps it (~3% slower on
-  // the adapters' SWA shape without it).
-  auto mid_sync = [] {
-    if constexpr (REL) __syncthreads();
+  // No barrier between the two phases of a slot: a tile is published, and
+  // its stage freed, at the odd slots' barriers alone; one there only kept
+  // the groups in step (without it: ~2% faster on C4 and 4x8192, ~9% with
+  // the fused bias at the adapters' shapes, outputs bitwise equal).
+  auto bias_first = [&] {
+    if constexpr (REL) {
+      bias_issue(k_lo);
+      bias_tile(sc, k_lo, std::true_type{});
+      bias_dma(k_lo + kBN);
+    }
   };
   if (grp_id == 0) {
+    bias_first();
     scores(0, sc);
-    bias_issue(k_lo);
-    softmax_phase(sc, k_lo, true, 0, [&] { bias_dma(k_lo + kBN); });
+    softmax_phase(sc, k_lo, true, none);
     for (int t = 0; t + 1 < ntiles; ++t) {
-      if constexpr (!REL) issue_tile(t + 3, (t + 3) & 3, t + 3 < ntiles);
+      issue_tile(t + 3, (t + 3) & 3, t + 3 < ntiles);
       mfma_phase(t, kWithS);
-      mid_sync();
-      // tile t+1's bias windows went out before tile t+2's DMA (t > 0)
-      softmax_phase(sc, k_lo + (t + 1) * kBN, false, t == 0 ? 0 : 4, [&] {
-        if constexpr (REL) {
-          bias_dma(k_lo + (t + 2) * kBN);
-          issue_tile(t + 3, (t + 3) & 3, t + 3 < ntiles);
-        }
-      });
+      softmax_phase(sc, k_lo + (t + 1) * kBN, false, none);
       odd_end(NB + 4);
     }
     mfma_phase(ntiles - 1, kNoS);
-    mid_sync();
     odd_end(0);   // everything, before the output goes through LDS
   } else {
-    if constexpr (!REL) issue_tile(3, 3, 3 < ntiles);
+    bias_first();
+    issue_tile(3, 3, 3 < ntiles);
     scores(0, sc);
-    bias_issue(k_lo);
-    softmax_phase(sc, k_lo, true, 0, [&] {
-      if constexpr (REL) {
-        bias_dma(k_lo + kBN);
-        issue_tile(3, 3, 3 < ntiles);
-      }
-    });
-    mid_sync();
+    softmax_phase(sc, k_lo, true, none);
     if (ntiles > 1) mfma_phase(0, kWithS);
     else mfma_phase(0, kNoS);
     odd_end(ntiles > 1 ? NB + 4 : 0);
     for (int t = 1; t + 1 < ntiles; ++t) {
-      softmax_phase(sc, k_lo + t * kBN, false, 4, [&] {
-        bias_dma(k_lo + (t + 1) * kBN);
-        issue_tile(t + 3, (t + 3) & 3, t + 3 < ntiles);
-      });
-      mid_sync();
+      softmax_phase(sc, k_lo + t * kBN, false,
+                    [&] { issue_tile(t + 3, (t + 3) & 3, t + 3 < ntiles); });
       mfma_phase(t, kWithS);
       odd_end(NB + 4);
     }
     if (ntiles > 1) {
       const int t = ntiles - 1;
-      softmax_phase(sc, k_lo + t * kBN, false, 4, none);
-      mid_sync();
+      softmax_phase(sc, k_lo + t * kBN, false, none);
       mfma_phase(t, kNoS);
       odd_end(0);   // the tile loads, before the output goes through LDS
     }

@@ -708,11 +708,18 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // The score accumulators of a bias tile start at rel[q, h, dist] / scale
   // for 0 <= dist < E, zero outside (the softmax multiplies by scale).
   // FAST (a whole tile with every dist in [0, E) for every query: no band
-  // test, every run starts inside its row) costs two byte-aligns per run
-  // and two instructions per score; the checked path handles the tiles at
+  // test, every run starts inside its row) costs a byte permute and a
+  // multiply per score; the checked path handles the tiles at
   // the diagonal, the run ends and the band edge. VMEM: the runs of the
   // first tile, whose loads start at the row when the run begins before it.
   [[maybe_unused]] const float inv_scale = REL ? 1.0f / a.scale : 0.0f;
+  // byte selectors (v_perm) that turn a run's dwords y0, y1, y2 into fp32
+  // values (bf16 in the high half, zeros below): with shift 0 the values
+  // are y1.hi, y1.lo, y0.hi, y0.lo, with shift 2 y2.lo, y1.hi, y1.lo, y0.hi;
+  // SEL_A picks the high half of the low dword of a pair (0) or the low
+  // half of its high dword (2), SEL_B the low (0) or high (2) half of one
+  [[maybe_unused]] const uint32_t sel_a = rel_sh ? 0x05040c0cu : 0x03020c0cu;
+  [[maybe_unused]] const uint32_t sel_b = rel_sh ? 0x03020c0cu : 0x01000c0cu;
   [[maybe_unused]] auto bias_init = [&](f32x16 (&s)[2], int kt,
                                         const u32x3 (&x)[8], auto fast_c,
                                         auto vmem_c) {
@@ -729,26 +736,23 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
           const int d0 = dq - 32 * kb - 8 * g;
           const uint32_t x0 = x[4 * kb + g][0], x1 = x[4 * kb + g][1],
                          x2 = x[4 * kb + g][2];
-          uint32_t w0, w1;
-          if constexpr (fast || !vmem) {
-            w0 = __builtin_amdgcn_alignbyte(x1, x0, rel_sh);
-            w1 = __builtin_amdgcn_alignbyte(x2, x1, rel_sh);
-          } else {
+          uint32_t y0 = x0, y1 = x1, y2 = x2;
+          if constexpr (!(fast || !vmem)) {
             const int b = rrow_b + 2 * (d0 - 3);
             const int b4 = b & ~3;
             // dwords the load started after the one holding rel[d0-3]
             // (only when that one lies before the row; 3 or more: every
             // dist of the run is negative, i.e. masked)
             const int kd = b4 < 0 ? (-b4) >> 2 : 0;
-            const uint32_t y0 = kd == 0 ? x0 : 0u;
-            const uint32_t y1 = kd == 0 ? x1 : (kd == 1 ? x0 : 0u);
-            const uint32_t y2 = kd == 0 ? x2 : (kd == 1 ? x1 : x0);
-            w0 = __builtin_amdgcn_alignbyte(y1, y0, rel_sh);
-            w1 = __builtin_amdgcn_alignbyte(y2, y1, rel_sh);
+            y0 = kd == 0 ? x0 : 0u;
+            y1 = kd == 0 ? x1 : (kd == 1 ? x0 : 0u);
+            y2 = kd == 0 ? x2 : (kd == 1 ? x1 : x0);
           }
           // element 4g + i is key0 + i, dist d0 - i
-          const uint32_t hv[4] = {w1 & 0xffff0000u, w1 << 16,
-                                  w0 & 0xffff0000u, w0 << 16};
+          const uint32_t hv[4] = {__builtin_amdgcn_perm(y2, y1, sel_a),
+                                  __builtin_amdgcn_perm(y1, y1, sel_b),
+                                  __builtin_amdgcn_perm(y1, y0, sel_a),
+                                  __builtin_amdgcn_perm(y0, y0, sel_b)};
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             float bias = __builtin_bit_cast(float, hv[i]);

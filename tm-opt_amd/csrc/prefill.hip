@@ -790,10 +790,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   for (int db = 0; db < 4; ++db) o_acc[db] = f32x16{};
   float m_run = -INFINITY;
   float l_part = 0.0f;
-  // Without a bias the max runs on the raw scores (scale > 0 commutes with
-  // max) and each probability is one fma + exp2: p = 2^(s*scale*log2e - m).
-  // (on tiles that carry the fused bias the scores are s*scale + bias,
-  // and the factor is log2e)
+  // The max runs on the raw scores (scale > 0 commutes with max; with the
+  // fused bias they hold q.k + bias / scale) and each probability is one
+  // fma + exp2: p = 2^(s*scale*log2e - m).
 
   // Lazy rescaling: the running max (log2 domain) only moves when the
   // tile's max exceeds it by more than kLazy, so probabilities stay below

@@ -655,7 +655,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
         for (int g = 0; g < 4; ++g) {
           const int b4 = (base - 64 * kb - 16 * g) & ~3;
           // before the first row (row 0 near dist 0): from the row start,
-          // shifted back into place by bias_apply
+          // shifted back into place by bias_init
           int off = band_tile ? (b4 < 0 ? 0 : b4) : kOob;
           asm volatile("" : "+v"(off));
           rb[4 * kb + g] = __builtin_bit_cast(

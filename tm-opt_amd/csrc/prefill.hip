@@ -589,9 +589,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // (key0 .. key0+3, dist d0 .. d0-3), whose four bf16 values are adjacent
   // in the row: the three dwords from the one holding rel[d0-3], realigned
   // by the lane's byte shift rel_sh.
-  // The first tile of an item loads its runs straight into registers (rb,
-  // 8 loads of 12 bytes before its scores). Every later tile goes through
-  // LDS: one MFMA phase ahead, each wave copies the 64-key window
+  // Every tile goes through LDS (the first one with the first K/V tiles,
+  // a later one one MFMA phase ahead): each wave copies the 64-key window
   // of each of its 32 rows (dists q-kt-63 .. q-kt, 32 dwords from the one
   // holding rel[q-kt-63]; a row whose values start mid-dword takes the 32
   // dwords from q-kt-64 and so lacks rel[q-kt]) into its 4 KB of LDS, two
@@ -606,12 +605,12 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // half's from the low half's same run), swapped across the lane halves.
   // The value a mid-dword row lacks, the third dword of the low half's
   // first run, is the first dword of the previous tile's window (`carry`,
-  // the high half's last run). The range check is per dword and the
-  // resource ends at a dword boundary, so every value of the rows arrives;
-  // dwords before a row or past the run read as zeros or as a neighbouring
-  // row's values, which lie outside the band and are dropped.
+  // the high half's last run; for the first tile, one load). The range
+  // check is per dword and the resource ends at a dword boundary, so every
+  // value of the rows arrives; dwords before a row or past the run read as
+  // zeros or as a neighbouring row's values, which lie outside the band
+  // and are dropped.
   typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-  [[maybe_unused]] u32x3 rb[8];
   [[maybe_unused]] uint32_t carry = 0;
   [[maybe_unused]] const uint32_t bb =
       lds0 + kNStage * kStage + (uint32_t)w * kBiasB;
@@ -637,33 +636,18 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     bias_a = (bb + 256u * (uint32_t)(l32 >> 1) + 128u * (uint32_t)(l32 & 1)) |
              (8u * (uint32_t)((l32 >> 1) ^ h2));
   }
-  // the first tile's runs, into registers
-  [[maybe_unused]] auto bias_issue = [&](int kt) {
+  // the first tile's carry: the dword after its window (the first of the
+  // window one tile before), loaded with the first tiles
+  [[maybe_unused]] auto bias_carry0 = [&] {
     if constexpr (REL) {
-      // (also when only the next tile is in the band: its first runs need
-      // this window's first dword)
-      const bool band_tile =
-          kt < k_hi && pos_lo - (kt + 2 * kBN - 1) < a.rel_extent;
-      // byte offset of rel[d0 - 3] for kb = g = 0, opaque to the compiler
-      // so that the eight offsets are derived from it here rather than
-      // hoisted out of the key loop as eight live registers
-      int base = rrow_b + 2 * (qpos - kt - 4 * h2 - 3);
-      asm volatile("" : "+v"(base));
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int b4 = (base - 64 * kb - 16 * g) & ~3;
-          // before the first row (row 0 near dist 0): from the row start,
-          // shifted back into place by bias_init
-          int off = band_tile ? (b4 < 0 ? 0 : b4) : kOob;
-          asm volatile("" : "+v"(off));
-          rb[4 * kb + g] = __builtin_bit_cast(
-              u32x3, __builtin_amdgcn_raw_buffer_load_b96(rrel, off, 0, 0));
-        }
+      const int x = rel_mis + l32 * (int)(a.r_st * 2) +
+                    2 * (prior + rel_row0 + l32 - 63);
+      int off = x - (x & 2) - 2 * k_lo + 128;
+      asm volatile("" : "+v"(off));
+      carry = __builtin_amdgcn_raw_buffer_load_b32(rrel, off, 0, 0);
     }
   };
-  // a later tile's windows, into LDS (always 16 DMAs; a tile neither in
+  // a tile's windows, into LDS (always 16 DMAs; a tile neither in
   // the band nor just before it, or past the run, fetches nothing)
   [[maybe_unused]] auto bias_dma_base = [&](int kt) {
     const bool live = kt < k_hi && pos_lo - (kt + 2 * kBN - 1) < a.rel_extent;
@@ -710,8 +694,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // FAST (a whole tile with every dist in [0, E) for every query: no band
   // test, every run starts inside its row) costs a byte permute and a
   // multiply per score; the checked path handles the tiles at
-  // the diagonal, the run ends and the band edge. VMEM: the runs of the
-  // first tile, whose loads start at the row when the run begins before it.
+  // the diagonal, the run ends and the band edge.
   [[maybe_unused]] const float inv_scale = REL ? 1.0f / a.scale : 0.0f;
   // byte selectors (v_perm) that turn a run's dwords y0, y1, y2 into fp32
   // values (bf16 in the high half, zeros below): with shift 0 the values
@@ -721,10 +704,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   [[maybe_unused]] const uint32_t sel_a = rel_sh ? 0x05040c0cu : 0x03020c0cu;
   [[maybe_unused]] const uint32_t sel_b = rel_sh ? 0x03020c0cu : 0x01000c0cu;
   [[maybe_unused]] auto bias_init = [&](f32x16 (&s)[2], int kt,
-                                        const u32x3 (&x)[8], auto fast_c,
-                                        auto vmem_c) {
+                                        const u32x3 (&x)[8], auto fast_c) {
     constexpr bool fast = decltype(fast_c)::value;
-    constexpr bool vmem = decltype(vmem_c)::value;
     if constexpr (REL) {
       // dist of the lane's first key for kb = g = 0 (opaque, as above)
       int dq = qpos - kt - 4 * h2;
@@ -736,18 +717,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
           const int d0 = dq - 32 * kb - 8 * g;
           const uint32_t x0 = x[4 * kb + g][0], x1 = x[4 * kb + g][1],
                          x2 = x[4 * kb + g][2];
-          uint32_t y0 = x0, y1 = x1, y2 = x2;
-          if constexpr (!(fast || !vmem)) {
-            const int b = rrow_b + 2 * (d0 - 3);
-            const int b4 = b & ~3;
-            // dwords the load started after the one holding rel[d0-3]
-            // (only when that one lies before the row; 3 or more: every
-            // dist of the run is negative, i.e. masked)
-            const int kd = b4 < 0 ? (-b4) >> 2 : 0;
-            y0 = kd == 0 ? x0 : 0u;
-            y1 = kd == 0 ? x1 : (kd == 1 ? x0 : 0u);
-            y2 = kd == 0 ? x2 : (kd == 1 ? x1 : x0);
-          }
+          const uint32_t y0 = x0, y1 = x1, y2 = x2;
           // element 4g + i is key0 + i, dist d0 - i
           const uint32_t hv[4] = {__builtin_amdgcn_perm(y2, y1, sel_a),
                                   __builtin_amdgcn_perm(y1, y1, sel_b),
@@ -857,43 +827,32 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   f32x16 sc[2];        // scores of the tile after the one being multiplied
   bf16x8 pf[2][2];     // probabilities of the tile being multiplied
 
-  // The bias of the tile at kt into its score accumulators: the first tile
-  // from its loads (FIRST), a later one from its windows in LDS, whose DMAs
-  // were followed by 4 tile DMAs at most; the windows are read before the
-  // next tile's DMAs into the same LDS go out (the carry is the last read).
-  [[maybe_unused]] auto bias_tile = [&](f32x16 (&s)[2], int kt, auto first_c) {
+  // The bias of the tile at kt into its score accumulators, from its
+  // windows in LDS, whose DMAs were followed by 4 tile DMAs at most; the
+  // windows are read before the next tile's DMAs into the same LDS go out
+  // (the carry is the last read).
+  [[maybe_unused]] auto bias_tile = [&](f32x16 (&s)[2], int kt)
+      __attribute__((always_inline)) {
     if constexpr (REL) {
-      constexpr bool first = decltype(first_c)::value;
       constexpr std::true_type kT{};
       constexpr std::false_type kF{};
+      // the bias band: some pair of the tile has dist = q - k < E (the
+      // smallest dist is pos_lo - (kt + 63))
       const bool with_bias = pos_lo - (kt + kBN - 1) < a.rel_extent;
       const bool fast = full_tile(kt) && pos_hi - kt < a.rel_extent;
-      if constexpr (first) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) asm volatile("" : "+v"(rb[i]));
-        carry = rb[7][0];
-        if (with_bias) {
-          if (fast) bias_init(s, kt, rb, kT, kT);
-          else bias_init(s, kt, rb, kF, kT);
-        } else {
-          s[0] = f32x16{};
-          s[1] = f32x16{};
-        }
+      wait_vm<4>();
+      asm volatile("" ::: "memory");   // the LDS reads stay below the wait
+      if (with_bias) {
+        u32x3 x[8];
+        bias_read(x);
+        if (fast) bias_init(s, kt, x, kT);
+        else bias_init(s, kt, x, kF);
       } else {
-        wait_vm<4>();
-        asm volatile("" ::: "memory");   // the LDS reads stay below the wait
-        if (with_bias) {
-          u32x3 x[8];
-          bias_read(x);
-          if (fast) bias_init(s, kt, x, kT, kF);
-          else bias_init(s, kt, x, kF, kF);
-        } else {
-          s[0] = f32x16{};
-          s[1] = f32x16{};
-          carry = lds_ld64(bias_a ^ 8u)[0];
-        }
-        asm volatile("" : "+v"(carry));
+        s[0] = f32x16{};
+        s[1] = f32x16{};
+        carry = lds_ld64(bias_a ^ 8u)[0];
       }
+      asm volatile("" : "+v"(carry));
     }
   };
 
@@ -955,7 +914,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     __builtin_amdgcn_s_setprio(1);
     [[maybe_unused]] uint32_t b2 = 0;
     if constexpr (with_s && REL) {
-      bias_tile(sc, k_lo + (t + 1) * kBN, std::false_type{});
+      bias_tile(sc, k_lo + (t + 1) * kBN);
       b2 = bias_dma_base(k_lo + (t + 2) * kBN);
     }
     const uint32_t vt_b = lds0 + (t & 3) * kStage + kTileB;
@@ -1030,6 +989,10 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   }
   issue_tile(0, 0);
   if (ntiles > 1) issue_tile(1, 1);
+  if constexpr (REL) {   // the first tile's bias windows and carry
+    bias_dma(k_lo);
+    bias_carry0();
+  }
   wait_vm<0>();
   __syncthreads();
 #pragma unroll
@@ -1068,10 +1031,11 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   // its stage freed, at the odd slots' barriers alone; one there only kept
   // the groups in step (without it: ~2% faster on C4 and 4x8192, ~9% with
   // the fused bias at the adapters' shapes, outputs bitwise equal).
+  // the first tile's bias (its windows came with the first tiles), then
+  // the second tile's windows
   auto bias_first = [&] {
     if constexpr (REL) {
-      bias_issue(k_lo);
-      bias_tile(sc, k_lo, std::true_type{});
+      bias_tile(sc, k_lo);
       bias_dma(k_lo + kBN);
     }
   };

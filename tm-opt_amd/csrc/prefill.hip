@@ -691,11 +691,18 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
       REL ? (uint32_t)((rrow_b + 2 * (qpos - 3)) & 3) : 0u;
   // The score accumulators of a bias tile start at rel[q, h, dist] / scale
   // for 0 <= dist < E, zero outside (the softmax multiplies by scale).
-  // FAST (a whole tile with every dist in [0, E) for every query: no band
-  // test, every run starts inside its row) costs a byte permute and a
-  // multiply per score; the checked path handles the tiles at
-  // the diagonal, the run ends and the band edge.
+  // FAST (no band test: a byte permute and a multiply per score) serves
+  // every tile whose scores outside the band are all masked anyway: a
+  // window no wider than the band (dist >= W is masked), or a tile whose
+  // dists stay below E for every query (dist < 0 is masked by causality);
+  // the value it leaves in a masked score is never used. The checked path
+  // (a tile across dist = E without such a window) zeroes the bias outside
+  // [0, E) per score.
   [[maybe_unused]] const float inv_scale = REL ? 1.0f / a.scale : 0.0f;
+  [[maybe_unused]] const bool band_masked =
+      a.window > 0 && a.window <= a.rel_extent;
+  // the band's width for this lane's query (0 past the run end)
+  [[maybe_unused]] const uint32_t e_q = qok ? (uint32_t)a.rel_extent : 0u;
   // byte selectors (v_perm) that turn a run's dwords y0, y1, y2 into fp32
   // values (bf16 in the high half, zeros below): with shift 0 the values
   // are y1.hi, y1.lo, y0.hi, y0.lo, with shift 2 y2.lo, y1.hi, y1.lo, y0.hi;
@@ -726,11 +733,8 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             float bias = __builtin_bit_cast(float, hv[i]);
-            if constexpr (!fast) {
-              const int dist = d0 - i;
-              const bool band = qok && dist >= 0 && dist < a.rel_extent;
-              bias = band ? bias : 0.0f;
-            }
+            if constexpr (!fast)   // 0 <= dist < E, one unsigned compare
+              bias = (uint32_t)(d0 - i) < e_q ? bias : 0.0f;
             s[kb][4 * g + i] = bias * inv_scale;
           }
         }
@@ -839,7 +843,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
       // the bias band: some pair of the tile has dist = q - k < E (the
       // smallest dist is pos_lo - (kt + 63))
       const bool with_bias = pos_lo - (kt + kBN - 1) < a.rel_extent;
-      const bool fast = full_tile(kt) && pos_hi - kt < a.rel_extent;
+      const bool fast = band_masked || pos_hi - kt < a.rel_extent;
       wait_vm<4>();
       asm volatile("" ::: "memory");   // the LDS reads stay below the wait
       if (with_bias) {

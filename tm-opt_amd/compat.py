@@ -240,6 +240,24 @@ def _append_rows(k, v, caches, lens):
     return rows
 
 
+_CU = {}
+
+
+def _uniform_cu(B, T, dev):
+    """cu_seqlens of B runs of T rows (0, T, .., B*T) as an int32 device
+    tensor, made once per (B, T, device) and reused, so that a call does not
+    spend a launch on it. Not kept when first made under a graph capture
+    (its memory would belong to that graph's pool)."""
+    key = (B, T, dev)
+    cu = _CU.get(key)
+    if cu is None:
+        cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=dev)
+        if not (dev.type == "cuda" and
+                torch.cuda.is_current_stream_capturing()):
+            _CU[key] = cu
+    return cu
+
+
 def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
                        block_m=64, block_n=64, caches=None, lens=None):
     """Fused prefill attention over in-batch K/V (attn_prefill.py:144).
@@ -296,7 +314,7 @@ def attn_prefill_fused(q, k, v, rel, q_positions, kv_positions, window,
         rt = rt.contiguous()
     relp = rt.as_strided((B * T, H, E), (rt.stride(1), rt.stride(2), 1))
     out = torch.empty((B, T, H, D), dtype=q.dtype, device=dev)
-    cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32, device=dev)
+    cu = _uniform_cu(B, T, dev)
     w = 0 if window is None else int(window)
     kr, vr = _kv_rows(k), _kv_rows(v)            # [B, T, HK, D]
     if caches is not None:

@@ -714,7 +714,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
                                         const u32x3 (&x)[8], auto fast_c) {
     constexpr bool fast = decltype(fast_c)::value;
     if constexpr (REL) {
-      // dist of the lane's first key for kb = g = 0 (opaque, as above)
+      // dist of the lane's first key for kb = g = 0 (opaque to the
+      // compiler, so that the runs' dists derive from it here instead of
+      // being hoisted out of the key loop as registers of their own)
       int dq = qpos - kt - 4 * h2;
       asm volatile("" : "+v"(dq));
 #pragma unroll

@@ -104,3 +104,16 @@ def test_ring_pool_detects_swapool_rows():
     assert compat._ring_pool([Ring(pk[1], pv[2])]) is None
     odd = torch.zeros((3, W, HK, 2 * D), dtype=torch.bfloat16)[..., :D]
     assert compat._ring_pool([Ring(odd[0], odd[1])]) is None
+
+
+def test_uniform_cu_made_once_per_shape():
+    """The fused adapter's run offsets (0, T, .., B*T) are made once per
+    (B, T, device) and reused, as an int32 tensor of B + 1 entries."""
+    compat = import_module("tm-opt_amd.compat")
+    dev = torch.device("cpu")
+    a = compat._uniform_cu(3, 5, dev)
+    assert a.dtype == torch.int32 and a.tolist() == [0, 5, 10, 15]
+    assert compat._uniform_cu(3, 5, dev) is a
+    b = compat._uniform_cu(3, 6, dev)
+    assert b is not a and b.tolist() == [0, 6, 12, 18]
+    assert compat._uniform_cu(1, 7, dev).tolist() == [0, 7]

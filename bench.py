@@ -226,7 +226,7 @@ def bench_mixed(tm, wl, steps, warmup):
             "us_prefill": parts["prefill"] * 1e3,
             "us_decode": parts["decode"] * 1e3,
             "decode_gbs": dec_b / (parts["decode"] * 1e-3) / 1e9,
-            "decode_workgroups": ms.num_workgroups,
+            "decode_workgroups": ms.wgs[name == "global"],
             "us_decode_standalone_grid": us_full,
             "decode_gbs_standalone_grid": dec_b / (us_full * 1e-6) / 1e9,
             "prefill_tflops": pf / (parts["prefill"] * 1e-3) / 1e12,

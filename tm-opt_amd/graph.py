@@ -137,27 +137,36 @@ class MixedStepGraph:
     the next layer). The decode's persistent work-groups hold their compute
     units for the whole decode, and a prefill work-group needs a whole
     compute unit's registers, so the decode's grid decides how the two
-    share the chip: beside a prefill it defaults to two thirds of its
-    stand-alone size (half the compute units). Measured on config 5: 30.6
-    ms per step, against 31.4 ms with the stand-alone grid (three quarters
-    of the compute units, which left the prefill a quarter of them while the
-    decode ran) and 31.7 ms without the second stream."""
+    share the chip. By default a global layer's decode (the longer one)
+    takes two thirds of its stand-alone size (half the compute units) and a
+    window layer's its stand-alone size (it is done in about half the time
+    of that layer's prefill and then leaves the prefill every unit).
+    Measured on config 5 (one box, four alternating runs each): 31.4-31.6
+    ms per step, against 31.8-32.8 ms with two thirds for both kinds; with
+    two thirds for both on another box 30.6 ms, against 31.4 ms with the
+    stand-alone grid for both and 31.7 ms without the second stream.
+    num_workgroups > 0 sets one grid for both kinds."""
 
     def __init__(self, step, min_pages=8, num_workgroups=0, overlap=True):
         self.s = step
         dev = step.q_decode.device
         B, HQ, D = step.q_decode.shape
         HKV = step.pools[0][0].shape[2]
-        if overlap and num_workgroups == 0:
-            num_workgroups = max(
-                1, attn.decode_default_workgroups(HKV) * 2 // 3)
+        full = attn.decode_default_workgroups(HKV)
+        if num_workgroups > 0:
+            self.wgs = {True: num_workgroups, False: num_workgroups}
+        elif overlap:
+            self.wgs = {True: max(1, full * 2 // 3), False: full}
+        else:
+            self.wgs = {True: full, False: full}
         self.n_chunks = len(step.chunk_lens)
         self.max_chunk = max(step.chunk_lens)
         self.out_p = torch.empty_like(step.q_prefill)
         self.out_d = torch.empty_like(step.q_decode)
         self.lse_d = torch.empty((B, HQ), dtype=torch.float32, device=dev)
-        self.ws = attn.decode_workspace(B, HQ, HKV, dev, num_workgroups)
-        self.min_pages, self.num_workgroups = min_pages, num_workgroups
+        self.ws = attn.decode_workspace(B, HQ, HKV, dev,
+                                        max(self.wgs.values()))
+        self.min_pages = min_pages
         self.overlap = overlap
         self.side = torch.cuda.Stream(device=dev) if overlap else None
         self.graph = StepGraph(self.run_eager, dev)
@@ -181,7 +190,7 @@ class MixedStepGraph:
             attn.decode_paged(s.q_decode, kp, vp, t[self.n_chunks:],
                               s.dec_ctx, s.scale, window=w,
                               min_pages=self.min_pages,
-                              num_workgroups=self.num_workgroups,
+                              num_workgroups=self.wgs[s.is_global[l]],
                               out=self.out_d, lse=self.lse_d,
                               workspace=self.ws)
 

@@ -22,7 +22,10 @@
  *   - Results are deterministic: fixed reduction order, no atomics.
  *
  * Supported shapes: D == 128, page_size == 16, HQ % HKV == 0 with
- * REP = HQ / HKV in {1, 2, 4, 8, 16} for decode and {1, 2, 4, 8} for prefill.
+ * REP = HQ / HKV in {1, 2, 4, 8, 16} for decode and any REP for prefill
+ * (the reference's H % HK == 0, attn_prefill.py:174; a REP other than 1, 2,
+ * 4 or 8 runs its query heads in groups of the largest of 8, 4, 2, 1
+ * dividing it, each group loading the keys once).
  * Other shapes return TMOPT_EUNSUPPORTED.
  */
 #ifndef TMOPT_ATTN_H

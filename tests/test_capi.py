@@ -71,15 +71,15 @@ def test_invalid_arguments_return_status(tm):
                                          null, p, 1 << 20, null)
         assert rc == tm._lib.TMOPT_EINVAL
         assert b"ring of 4 pages" in lib.tmopt_last_error()
-    # prefill: REP 3 and 16 are unsupported (1, 2, 4 and 8 are)
-    for hq in (12, 64):
-        rc = lib.tmopt_attn_prefill_varlen(p, 0, 0, p, 0, 0, 0, 1, p, 0, 0,
-                                           0, 1, p, null, 1, 4, null, null,
-                                           null, 0, 0, 16, 0, hq, 4, 128, 0,
-                                           0.1, null, 0, 0, 0, p, 0, 0, null,
-                                           null, null)
-        assert rc == tm._lib.TMOPT_EUNSUPPORTED, hq
-        assert b"not in {1, 2, 4, 8}" in lib.tmopt_last_error()
+    # prefill: any HQ % HKV == 0 ratio; one that would need more than 65535
+    # scheduled KV heads (groups of up to 8 query heads) is refused
+    rc = lib.tmopt_attn_prefill_varlen(p, 0, 0, p, 0, 0, 0, 1, p, 0, 0,
+                                       0, 1, p, null, 1, 4, null, null,
+                                       null, 0, 0, 16, 0, 3 * 30000, 30000,
+                                       128, 0, 0.1, null, 0, 0, 0, p, 0, 0,
+                                       null, null, null)
+    assert rc == tm._lib.TMOPT_EUNSUPPORTED
+    assert b"exceeds 65535" in lib.tmopt_last_error()
 
     def prefill(k, prior, table, wrap, window):
         return lib.tmopt_attn_prefill_varlen(

@@ -74,7 +74,7 @@ def test_attn_global_flat_rows(tm, dev):
 
 
 @pytest.mark.parametrize("window,E", [(None, 1024), (64, 64)])
-@pytest.mark.parametrize("hq,hk", [(32, 4), (64, 16)])
+@pytest.mark.parametrize("hq,hk", [(32, 4), (64, 16), (48, 4)])
 @pytest.mark.parametrize("T", [200, 77])
 def test_attn_prefill_fused_padded_batch(tm, dev, window, E, hq, hk, T):
     """T = 200: the kernel reads the channel-major K/V in place (runs of

@@ -2,7 +2,8 @@
 
 Tolerances: outputs max-abs 2e-2 / rtol 1e-2, LSE 1e-3.
 Covers ragged lengths around the 32-query / 64-key tile edges, causal and
-windowed masks, GQA 1, 2, 4 and 8, strided inputs, chunked prefill reading prior
+windowed masks, GQA 1, 2, 4 and 8 (and 3, 5, 6, 12, 16, 24, run as groups
+of 8, 4, 2 or 1 query heads per stored KV head), strided inputs, chunked prefill reading prior
 context from a shuffled paged cache, the fused relative bias (band shorter
 than the runs, so most key tiles carry none; packed and paged sources), the
 q = 0 closed form (LSE = ln(#visible keys)), determinism, config 4 at full
@@ -36,7 +37,8 @@ def _gpu(tm, case, dev, **kw):
 
 
 @pytest.mark.parametrize("window", [0, 1, 17, 64, 100])
-@pytest.mark.parametrize("hq,hkv", [(32, 4), (64, 16), (8, 8), (16, 8)])
+@pytest.mark.parametrize("hq,hkv", [(32, 4), (64, 16), (8, 8), (16, 8),
+                                    (12, 4), (64, 4), (5, 1)])
 def test_ragged_lengths(tm, dev, window, hq, hkv):
     case = _wl().make_prefill("ragged", 21, lens=LENS, window=window, hq=hq,
                               hkv=hkv)
@@ -50,7 +52,7 @@ def test_ragged_lengths(tm, dev, window, hq, hkv):
 
 @pytest.mark.parametrize("hq,hkv", [(8, 1), (16, 2), (24, 3), (32, 4),
                                     (64, 16), (4, 4), (6, 3), (16, 16),
-                                    (24, 12)])
+                                    (24, 12), (12, 4), (40, 8), (96, 4)])
 def test_every_row_written(tm, dev, hq, hkv):
     """The work-group -> (KV head, run, query block) schedule covers every
     row: 70 runs (more than one wave's worth of runs) of ragged lengths,
@@ -116,7 +118,8 @@ def test_output_rows_8_byte_aligned(tm, dev):
 
 
 @pytest.mark.parametrize("window", [0, 48])
-@pytest.mark.parametrize("HQ,HKV", [(32, 4), (8, 8), (8, 4)])
+@pytest.mark.parametrize("HQ,HKV", [(32, 4), (8, 8), (8, 4), (24, 2),
+                                    (6, 2)])
 def test_paged_prior_context(tm, dev, window, HQ, HKV):
     """Chunked prefill: each run's keys = prior context + its own tokens,
     all in a shuffled page pool (written by the KV-write kernel)."""
@@ -239,7 +242,8 @@ def test_one_long_run_sampled_rows(tm, dev):
 
 
 @pytest.mark.parametrize("E,window", [(95, 0), (1, 0), (80, 256), (300, 64)])
-@pytest.mark.parametrize("hq,hkv", [(32, 4), (64, 16), (8, 8), (8, 4)])
+@pytest.mark.parametrize("hq,hkv", [(32, 4), (64, 16), (8, 8), (8, 4),
+                                    (12, 4), (64, 4)])
 def test_bias_band_shorter_than_runs(tm, dev, E, window, hq, hkv):
     """Fused bias rel[t, h, dist] inside 0 <= dist < E: with E well below
     the run lengths most key tiles lie wholly outside the band and skip the
@@ -386,7 +390,7 @@ def _packed_own(k_all, lens, prior):
 
 
 @pytest.mark.parametrize("source", ["paged", "mixed"])
-@pytest.mark.parametrize("hq,hkv", [(32, 4), (64, 16)])
+@pytest.mark.parametrize("hq,hkv", [(32, 4), (64, 16), (12, 4)])
 def test_window_never_reads_before_it(tm, dev, source, hq, hkv):
     """Windowed chunked prefill over a pool whose keys before each run's
     first visible position (prior - W + 1) are NaN, pages wholly before it

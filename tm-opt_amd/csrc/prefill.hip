@@ -131,7 +131,12 @@ struct PrefillArgs {
   int table_wrap;    // > 0: each table row is a ring of that many pages
   int num_pages;
   int page_size;
-  int HQ, HKV;
+  int HQ;
+  int HKV;           // KV heads as scheduled (virtual, see kv_div)
+  int kv_div;        // scheduled KV heads per stored one: 1 unless HQ/HKV
+                     // is not 1, 2, 4 or 8 (then each stored head serves
+                     // kv_div groups of up to 8 query heads)
+  int HKV_stored;    // KV heads of the k/v rows and the pools
   int window;
   float scale;
   float scale_log2;
@@ -293,6 +298,7 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   const Work wk = schedule(a, BQ, lane);
   if (wk.seq < 0) return;
   const int kvh = wk.kvh;
+  const int kvs = kvh / a.kv_div;   // the stored KV head its keys come from
   const int seq = wk.seq;
   const int qb = wk.qb;
 
@@ -356,9 +362,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
       // outside the resource and arrive as zeros.
       kst_b = (int)(a.k_sd * 2);
       vst_b = (int)(a.v_sd * 2);
-      rk = make_rsrc(a.k + k0 + (int64_t)kvh * a.k_sh,
+      rk = make_rsrc(a.k + k0 + (int64_t)kvs * a.k_sh,
                         (uint32_t)(((int64_t)(kD - 1) * a.k_sd + len) * 2));
-      rv = make_rsrc(a.v + v0 + (int64_t)kvh * a.v_sh,
+      rv = make_rsrc(a.v + v0 + (int64_t)kvs * a.v_sh,
                         (uint32_t)(((int64_t)(kD - 1) * a.v_sd + len) * 2));
       const int r = 8 * w + (lane >> 3);
       const int c = (lane & 7) ^ cm_sig(r);
@@ -368,9 +374,9 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
     } else {
       kst_b = (int)(a.k_st * 2);
       vst_b = (int)(a.v_st * 2);
-      rk = make_rsrc(a.k + k0 + (int64_t)kvh * a.k_sh,
+      rk = make_rsrc(a.k + k0 + (int64_t)kvs * a.k_sh,
                         (uint32_t)(((int64_t)(len - 1) * a.k_st + kD) * 2));
-      rv = make_rsrc(a.v + v0 + (int64_t)kvh * a.v_sh,
+      rv = make_rsrc(a.v + v0 + (int64_t)kvs * a.v_sh,
                         (uint32_t)(((int64_t)(len - 1) * a.v_st + kD) * 2));
       klane_p = grp * kst_b + 16 * kchunk;
       vlane_p = grp * vst_b + 16 * vchunk;
@@ -378,12 +384,12 @@ __global__ __launch_bounds__(512) void prefill_kernel(PrefillArgs a) {
   }
   // pool rows: keys below `plim` (all keys on the paged source, the prior
   // context on the mixed one)
-  [[maybe_unused]] const int row_b = a.HKV * kD * 2;   // one token row
+  [[maybe_unused]] const int row_b = a.HKV_stored * kD * 2;   // one token row
   [[maybe_unused]] const int64_t page_b = (int64_t)kPage * row_b;
   [[maybe_unused]] int klane = 0, vlane = 0;
   if constexpr (POOL) {
-    klane = grp * row_b + kvh * (kD * 2) + 16 * kchunk;
-    vlane = grp * row_b + kvh * (kD * 2) + 16 * vchunk;
+    klane = grp * row_b + kvs * (kD * 2) + 16 * kchunk;
+    vlane = grp * row_b + kvs * (kD * 2) + 16 * vchunk;
   }
   [[maybe_unused]] const int32_t __attribute__((address_space(4)))* trow =
       POOL ? as_const(a.bt) + (int64_t)seq * a.bt_stride : nullptr;
@@ -1221,10 +1227,15 @@ extern "C" int tmopt_attn_prefill_varlen(
   TMOPT_REQUIRE(D == kD, TMOPT_EUNSUPPORTED, "prefill: D=%d (only 128)", D);
   TMOPT_REQUIRE(HKV > 0 && HQ > 0 && HQ % HKV == 0 && HKV <= 65535,
                 TMOPT_EINVAL, "prefill: HQ=%d HKV=%d", HQ, HKV);
-  const int rep = HQ / HKV;
-  TMOPT_REQUIRE(rep == 1 || rep == 2 || rep == 4 || rep == 8,
-                TMOPT_EUNSUPPORTED, "prefill: HQ/HKV=%d not in {1, 2, 4, 8}",
-                rep);
+  // Query heads per work-group: the largest of 8, 4, 2, 1 dividing HQ/HKV;
+  // a ratio above it runs as kv_div scheduled heads per stored KV head
+  // (its keys then load once per group of `rep` query heads).
+  const int ratio = HQ / HKV;
+  const int rep = ratio % 8 == 0 ? 8 : ratio % 4 == 0 ? 4 : ratio % 2 == 0 ? 2 : 1;
+  const int kv_div = ratio / rep;
+  TMOPT_REQUIRE((int64_t)HKV * kv_div <= 65535, TMOPT_EUNSUPPORTED,
+                "prefill: HKV=%d x %d query-head groups exceeds 65535", HKV,
+                kv_div);
   TMOPT_REQUIRE(window >= 0, TMOPT_EINVAL, "prefill: window=%d", window);
   TMOPT_REQUIRE(scale > 0.0f, TMOPT_EINVAL, "prefill: scale must be > 0");
   TMOPT_REQUIRE(rel == nullptr || rel_extent > 0, TMOPT_EINVAL,
@@ -1240,7 +1251,8 @@ extern "C" int tmopt_attn_prefill_varlen(
   {
     const int bq = 256 / rep;
     const int64_t blocks =
-        (int64_t)HKV * num_seqs * ((max_seqlen_q + bq - 1) / bq) + 8 * 8;
+        (int64_t)HKV * kv_div * num_seqs * ((max_seqlen_q + bq - 1) / bq) +
+        8 * 8;
     TMOPT_REQUIRE(blocks < 0x7fffffffll, TMOPT_EUNSUPPORTED,
                   "prefill: %lld work-groups exceed the grid limit",
                   (long long)blocks);
@@ -1355,7 +1367,9 @@ extern "C" int tmopt_attn_prefill_varlen(
   a.num_pages = num_pages > 0x7fffffff ? 0x7fffffff : (int)num_pages;
   a.page_size = page_size > 0 ? page_size : 16;
   a.HQ = HQ;
-  a.HKV = HKV;
+  a.HKV = HKV * kv_div;
+  a.kv_div = kv_div;
+  a.HKV_stored = HKV;
   a.window = window;
   a.scale = scale;
   a.scale_log2 = scale * kLog2e;

@@ -22,10 +22,12 @@
  *   - Results are deterministic: fixed reduction order, no atomics.
  *
  * Supported shapes: D == 128, page_size == 16, HQ % HKV == 0 with
- * REP = HQ / HKV in {1, 2, 4, 8, 16} for decode and any REP for prefill
- * (the reference's H % HK == 0, attn_prefill.py:174; a REP other than 1, 2,
- * 4 or 8 runs its query heads in groups of the largest of 8, 4, 2, 1
- * dividing it, each group loading the keys once).
+ * any REP = HQ / HKV (the reference's H % HK == 0, attn_prefill.py:174).
+ * Decode reads each KV head's pages once for up to 16 query heads; a
+ * larger REP runs in groups of its largest divisor up to 16, each group
+ * reading the pages once. Prefill stages keys once for up to 8 query heads;
+ * a REP that 8, 4 or 2 does not divide runs in groups of the largest of
+ * them (or 1) dividing it, each group loading the keys once.
  * Other shapes return TMOPT_EUNSUPPORTED.
  */
 #ifndef TMOPT_ATTN_H

@@ -63,6 +63,14 @@ def test_invalid_arguments_return_status(tm):
                                      1, 0, 0.1, null, 0, 8, 0, p, null, p,
                                      1 << 20, null)
     assert rc == tm._lib.TMOPT_EUNSUPPORTED
+    # decode: any HQ % HKV == 0 ratio; a prime one above 16 runs as one
+    # scheduled KV head per query head, and beyond 65535 of them it is
+    # refused
+    rc = lib.tmopt_attn_decode_paged(p, p, p, p, 1, 0, p, 1, 17 * 30000,
+                                     30000, 128, 16, 1, 0, 0.1, null, 0, 8,
+                                     0, p, null, p, 1 << 20, null)
+    assert rc == tm._lib.TMOPT_EUNSUPPORTED
+    assert b"exceeds 65535" in lib.tmopt_last_error()
     # decode: a ring table of 4 pages (64 positions) with no window, then
     # with a window wider than the ring
     for window in (0, 65):

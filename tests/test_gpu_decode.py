@@ -59,8 +59,12 @@ def test_edge_positions(tm, dev, window, min_pages, wgs):
 
 
 @pytest.mark.parametrize("hq,hkv", [(64, 8), (64, 16), (32, 4), (16, 16),
-                                    (32, 2)])
+                                    (32, 2), (12, 4), (6, 1), (15, 1),
+                                    (96, 4), (64, 1), (17, 1), (40, 2)])
 def test_gqa_shapes(tm, dev, hq, hkv):
+    """GQA 1, 2, 4, 8, 16; ratios up to 16 that are not powers of two (3,
+    6, 15: one read of the pages per KV head); ratios above 16 (24, 64, 17,
+    20: groups of 8, 16, 1, 10 query heads per scheduled KV head)."""
     from importlib import import_module
     wl = import_module("tm-opt_amd.workloads")
     case = wl.make_decode("gqa", 8, 6, 1, 700, 0, hq=hq, hkv=hkv)
@@ -114,11 +118,13 @@ def test_zero_query_closed_form(tm, dev):
     assert_out_close(out, ref_o, "q=0")
 
 
-def test_rel_bias_and_ring_table(tm, dev):
+@pytest.mark.parametrize("HQ,HK", [(64, 16), (48, 4), (96, 4)])
+def test_rel_bias_and_ring_table(tm, dev, HQ, HK):
     """The reference's SWA model semantics (attn_swa.py:120-141): ring pool
-    [S, W, HK, D] viewed as pages, scale 1/D, fused rel bias of extent W."""
+    [S, W, HK, D] viewed as pages, scale 1/D, fused rel bias of extent W;
+    GQA 4, 12 and 24."""
     g = torch.Generator().manual_seed(5)
-    S, W, HK, D, HQ = 6, 512, 16, 128, 64
+    S, W, D = 6, 512, 128
     pool_k = torch.randn((S + 1, W, HK, D), generator=g).to(torch.bfloat16)
     pool_v = torch.randn((S + 1, W, HK, D), generator=g).to(torch.bfloat16)
     pos = torch.tensor([0, 3, 200, 511, 512, 513, 800, 0])
@@ -137,8 +143,8 @@ def test_rel_bias_and_ring_table(tm, dev):
                                window=W, table_wrap=per, rel=rel.to(dev),
                                min_pages=2)
     torch.cuda.synchronize()
-    assert_out_close(out, ref_o, "ring+rel")
-    assert_lse_close(lse, ref_l, "ring+rel")
+    assert_out_close(out, ref_o, f"ring+rel {HQ}/{HK}")
+    assert_lse_close(lse, ref_l, f"ring+rel {HQ}/{HK}")
 
 
 @pytest.mark.parametrize("k,wgs", [(1, 40), (3, 14), (7, 6), (40, 1)])

@@ -42,7 +42,9 @@
 //    lane owns 8 scores of one head: the running max needs two cross-lane
 //    steps (xor 16, xor 32) and the running sum stays lane-local until the
 //    end of a piece. P^T is then already in the B-operand layout of
-//    O^T = V^T.P^T.
+//    O^T = V^T.P^T. Any GQA ratio up to 16 fills that many columns (one
+//    read of the pages); a larger one runs as groups of its largest divisor
+//    up to 16, each group a scheduled KV head of its own.
 //
 // Per step (two pages = 32 tokens, tile t = page t):
 //  Load i of tile t brings tokens 16t + 4i + (lane >> 4), 16 bytes (dims
@@ -88,7 +90,8 @@ struct DecodeArgs {
   int bt_kind;
   const int64_t* rows64;
   const int64_t* pos64;
-  int B, HQ, HKV;
+  int B, HQ;
+  int HKV;           // KV heads as scheduled (HKV_stored * kv_div)
   int num_pages;     // clamped to INT32_MAX: page ids are int32
   int window;
   float scale_log2;  // scale * log2(e)
@@ -102,6 +105,13 @@ struct DecodeArgs {
   float* part_o;     // [B + G, HQ, D] fp32
   float* part_lse;   // [B + G, HQ]
   int* geo;          // [B + 2]: C, then the page-stream prefix pref[0..B]
+  // read by the REP 0 kernels only (any other REP implies rep == REP,
+  // kv_div == 1, HKV_stored == HKV)
+  int rep;           // query heads per scheduled KV head (1..16)
+  int kv_div;        // scheduled KV heads per stored one: 1 unless HQ/HKV
+                     // is above 16 (then kv_div groups of `rep` query
+                     // heads each read the stored head's pages)
+  int HKV_stored;    // KV heads of a pool token row
 };
 
 __device__ __forceinline__ int vis_lo(int n, int window) {
@@ -305,8 +315,12 @@ void decode_kernel(DecodeArgs a) {
     u0 = min(wg * C, U);
     u1 = min(u0 + C, U);
   }
-  const int hq = kvh * REP + r;  // query head owned as MFMA column r
-  const bool head_ok = r < REP;
+  // REP 1, 2, 4, 8, 16: that many query heads per KV head; REP 0: a.rep
+  // of them (any count up to the 16 MFMA columns) and a.kv_div scheduled
+  // heads per stored one
+  const int rep = REP > 0 ? REP : a.rep;
+  const int hq = kvh * rep + r;  // query head owned as MFMA column r
+  const bool head_ok = r < rep;
 
   // ---- 2. sequences with no visible key: output 0, LSE -inf -------------
   for (int b = wg; b < a.B; b += G) {
@@ -366,11 +380,12 @@ void decode_kernel(DecodeArgs a) {
     last_b = cb;
   };
 
-  const int row_elems = a.HKV * kD;
+  const int row_elems = (REP > 0 ? a.HKV : a.HKV_stored) * kD;
   const int page_bytes = kPS * row_elems * 2;
-  // byte offset of (token lane >> 4, head kvh, dims 8 (lane & 15)..) in a
+  const int kvs = REP > 0 ? kvh : kvh / a.kv_div;   // the stored KV head
+  // byte offset of (token lane >> 4, head kvs, dims 8 (lane & 15)..) in a
   // page
-  const int lane_off = ((lane >> 4) * row_elems + kvh * kD + 8 * (lane & 15)) * 2;
+  const int lane_off = ((lane >> 4) * row_elems + kvs * kD + 8 * (lane & 15)) * 2;
   // this wave's LDS tiles: 32 token rows of 256 B each for K, then for V.
   // K row x keeps 16-byte chunk c at slot c ^ (x & 15), V row x keeps
   // 32-byte unit u at slot u ^ (x & 7): conflict-free for the row writes,
@@ -770,10 +785,16 @@ static int decode_impl(
                 "decode: page_size=%d (only 16)", page_size);
   TMOPT_REQUIRE(HKV > 0 && HQ > 0 && HQ % HKV == 0, TMOPT_EINVAL,
                 "decode: HQ=%d HKV=%d", HQ, HKV);
-  const int rep = HQ / HKV;
-  TMOPT_REQUIRE(rep == 1 || rep == 2 || rep == 4 || rep == 8 || rep == 16,
-                TMOPT_EUNSUPPORTED, "decode: HQ/HKV=%d not in {1,2,4,8,16}",
-                rep);
+  // Query heads per scheduled KV head: the whole ratio up to 16 (the MFMA
+  // columns), else its largest divisor up to 16, the stored head then
+  // scheduled kv_div times (each reading its pages once per group).
+  const int ratio = HQ / HKV;
+  int rep = ratio;
+  while (rep > 16 || ratio % rep != 0) --rep;
+  const int kv_div = ratio / rep;
+  TMOPT_REQUIRE((int64_t)HKV * kv_div <= 65535, TMOPT_EUNSUPPORTED,
+                "decode: HKV=%d x %d query-head groups exceeds 65535", HKV,
+                kv_div);
   TMOPT_REQUIRE((int64_t)kPS * HKV * kD * 2 < (1ll << 31), TMOPT_EUNSUPPORTED,
                 "decode: page too large");
   TMOPT_REQUIRE(num_pages > 0 && bt_stride > 0 && table_wrap >= 0 &&
@@ -826,7 +847,10 @@ static int decode_impl(
   a.pos64 = pos64;
   a.B = B;
   a.HQ = HQ;
-  a.HKV = HKV;
+  a.HKV = HKV * kv_div;
+  a.rep = rep;
+  a.kv_div = kv_div;
+  a.HKV_stored = HKV;
   a.num_pages = num_pages > 0x7fffffff ? 0x7fffffff : (int)num_pages;
   a.window = window;
   a.scale_log2 = scale * kLog2e;
@@ -840,17 +864,18 @@ static int decode_impl(
   a.part_lse = (float*)((char*)workspace + off_lse);
   a.geo = (int*)((char*)workspace + off_geo);
 
-  const int nw = waves_per_wg(HKV);
+  const int nw = waves_per_wg(a.HKV);
   const size_t tab = ((size_t)B + 1 + 4) * sizeof(int);
   const size_t tiles = (size_t)nw * kWaveLds;
   const size_t lds = tab > tiles ? tab : tiles;
   hipStream_t st = (hipStream_t)stream;
-  switch (rep) {
+  switch (kv_div == 1 ? rep : 0) {
     case 1: launch<1>(a, G, nw, lds, st); break;
     case 2: launch<2>(a, G, nw, lds, st); break;
     case 4: launch<4>(a, G, nw, lds, st); break;
     case 8: launch<8>(a, G, nw, lds, st); break;
-    default: launch<16>(a, G, nw, lds, st); break;
+    case 16: launch<16>(a, G, nw, lds, st); break;
+    default: launch<0>(a, G, nw, lds, st); break;
   }
   int rc = check_launch("decode");
   if (rc || seqs_per_wg > 0) return rc;   // whole sequences: nothing to merge

@@ -117,3 +117,40 @@ def test_uniform_cu_made_once_per_shape():
     b = compat._uniform_cu(3, 6, dev)
     assert b is not a and b.tolist() == [0, 6, 12, 18]
     assert compat._uniform_cu(1, 7, dev).tolist() == [0, 7]
+
+
+def _run_bench(*args, env_extra=None):
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = dict(os.environ, **(env_extra or {}))
+    return subprocess.run([sys.executable, os.path.join(root, "bench.py"),
+                           *args], capture_output=True, text=True, env=env,
+                          timeout=120, cwd=root)
+
+
+@pytest.mark.parametrize("args,env_extra", [
+    (("--gpus", "2"), None),
+    (("--gpus", "8", "--steps", "3"), None),
+    ((), {"WORLD_SIZE": "2"}),
+])
+def test_bench_refuses_more_than_one_gpu(args, env_extra):
+    """bench.py measures one GPU: --gpus above 1, or a launcher's
+    WORLD_SIZE above 1, ends with status 2 and a message saying so, before
+    any GPU is touched (and prints no JSON line)."""
+    r = _run_bench(*args, env_extra=env_extra)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
+    assert r.stdout.strip() == ""
+
+
+def test_bench_fails_loudly_without_a_gpu():
+    """Without a visible GPU the bench exits non-zero instead of timing a
+    fallback (this container has none; skipped where one is visible)."""
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    r = _run_bench("--steps", "1", "--warmup", "0")
+    assert r.returncode == 1
+    assert "no GPU" in r.stderr
+    assert r.stdout.strip() == ""
